@@ -1,0 +1,223 @@
+"""ctypes bindings for the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker / timed CPU
+baseline.  The product package never imports it.
+
+``Oracle`` wraps oracle/liboracle.so (plain-C restatement, ung_oracle.c);
+``RefOracle`` wraps oracle/_ref/libungref.so (the reference's own
+distance.cpp + search_queue.cpp compiled from /root/reference, see
+oracle/Makefile), when that library has been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libungref.so")
+
+_u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+
+
+def _u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Oracle:
+    """Plain-C restatement of the reference CPU semantics."""
+
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (run `make -C oracle`)")
+        L = C.CDLL(path)
+        L.ungo_l2.restype = C.c_float
+        L.ungo_l2.argtypes = [_f32p, _f32p, C.c_uint32]
+        L.ungo_l2_f64.restype = C.c_double
+        L.ungo_l2_f64.argtypes = [_f32p, _f32p, C.c_uint32]
+        L.ungo_queue_insert.restype = C.c_int
+        L.ungo_queue_insert.argtypes = [_u32p, _f32p, C.POINTER(C.c_int32), C.c_int32,
+                                        C.c_uint32, C.c_float]
+        L.ungo_divide_groups.restype = C.c_uint32
+        L.ungo_divide_groups.argtypes = [C.c_uint32, _u32p, _u32p, _u32p, _u32p, _u32p]
+        L.ungo_min_supersets.restype = C.c_int64
+        L.ungo_min_supersets.argtypes = [C.c_uint32, _u32p, _u32p, _u32p, _u32p, C.c_int64]
+        L.ungo_cross_exact.restype = None
+        L.ungo_cross_exact.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, _u32p, _u32p,
+                                       _u32p, C.c_uint32, _u32p, _f32p, _i32p, C.c_int]
+        L.ungo_cross_exact_points.restype = None
+        L.ungo_cross_exact_points.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, _u32p,
+                                              _u32p, _u32p, _u32p, _u32p, C.c_uint32, C.c_uint32,
+                                              _u32p, _f32p, _i32p, C.c_int]
+        L.ungo_intra_exact.restype = None
+        L.ungo_intra_exact.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                       _u32p, _f32p, C.c_int]
+        L.ungo_pack_anchor_row.restype = None
+        L.ungo_pack_anchor_row.argtypes = [_u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                           C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                           C.c_uint32, _u32p]
+        self.lib = L
+
+    # -- distances -------------------------------------------------------
+    def l2(self, a, b) -> float:
+        a, b = _f32(a), _f32(b)
+        return float(self.lib.ungo_l2(a, b, a.shape[0]))
+
+    def l2_f64(self, a, b) -> float:
+        a, b = _f32(a), _f32(b)
+        return float(self.lib.ungo_l2_f64(a, b, a.shape[0]))
+
+    # -- queue -----------------------------------------------------------
+    def queue_stream(self, ids, dists, cap):
+        qi = np.zeros(cap + 1, np.uint32)
+        qd = np.zeros(cap + 1, np.float32)
+        size = C.c_int32(0)
+        for i, d in zip(np.asarray(ids, np.uint32), np.asarray(dists, np.float32)):
+            self.lib.ungo_queue_insert(qi, qd, C.byref(size), cap, int(i), float(d))
+        return qi[: size.value].copy(), qd[: size.value].copy()
+
+    # -- groups / LNG -----------------------------------------------------
+    def divide_groups(self, lab_ptr, lab_idx):
+        lab_ptr, lab_idx = _u32(lab_ptr), _u32(lab_idx)
+        n = lab_ptr.shape[0] - 1
+        pg = np.zeros(max(n, 1), np.uint32)
+        gb = np.zeros(n + 2, np.uint32)
+        n2o = np.zeros(max(n, 1), np.uint32)
+        G = self.lib.ungo_divide_groups(n, lab_ptr, lab_idx if lab_idx.size else np.zeros(1, np.uint32), pg, gb, n2o)
+        return int(G), pg[:n], gb[: G + 2], n2o[:n]
+
+    def min_supersets(self, set_ptr, set_idx):
+        set_ptr, set_idx = _u32(set_ptr), _u32(set_idx)
+        G = set_ptr.shape[0] - 2
+        cap = max(16, G * 64)
+        while True:
+            out_ptr = np.zeros(G + 2, np.uint32)
+            out_idx = np.zeros(cap, np.uint32)
+            tot = self.lib.ungo_min_supersets(G, set_ptr, set_idx if set_idx.size else np.zeros(1, np.uint32),
+                                              out_ptr, out_idx, cap)
+            if tot >= 0:
+                return out_ptr, out_idx[:tot].copy()
+            cap *= 4
+
+    # -- builders ----------------------------------------------------------
+    def cross_exact(self, X, group_begin, in_ptr, in_idx, k, nthreads=0):
+        X = _f32(X)
+        N, d = X.shape
+        G = group_begin.shape[0] - 2
+        ids = np.zeros((N, k), np.uint32)
+        dists = np.zeros((N, k), np.float32)
+        size = np.zeros(N, np.int32)
+        in_idx = _u32(in_idx) if len(in_idx) else np.zeros(1, np.uint32)
+        self.lib.ungo_cross_exact(X, N, d, G, _u32(group_begin), _u32(in_ptr), in_idx,
+                                  k, ids, dists, size, nthreads)
+        return ids, dists, size
+
+    def cross_exact_points(self, X, group_begin, point_group, out_ptr, out_idx, q_list, k, nthreads=0):
+        X = _f32(X)
+        N, d = X.shape
+        G = group_begin.shape[0] - 2
+        q_list = _u32(q_list)
+        nq = q_list.shape[0]
+        ids = np.zeros((nq, k), np.uint32)
+        dists = np.zeros((nq, k), np.float32)
+        size = np.zeros(nq, np.int32)
+        out_idx = _u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
+        self.lib.ungo_cross_exact_points(X, N, d, G, _u32(group_begin), _u32(point_group),
+                                         _u32(out_ptr), out_idx, q_list, nq, k, ids, dists, size,
+                                         nthreads)
+        return ids, dists, size
+
+    def intra_exact(self, X, begin, n, K, nthreads=0):
+        X = _f32(X)
+        ids = np.zeros((n, K), np.uint32)
+        dists = np.zeros((n, K), np.float32)
+        self.lib.ungo_intra_exact(X, X.shape[1], begin, n, K, ids, dists, nthreads)
+        return ids, dists
+
+    def pack_anchor_row(self, top_idx, cand_degree, n, local_src, final_degree, head_keep,
+                        anchor_tail=1, anchor_slots=0, bidir_anchor=0, graph_stride=None):
+        if graph_stride is None:
+            graph_stride = final_degree + 1
+        top = _u32(top_idx) if len(top_idx) else np.zeros(1, np.uint32)
+        row = np.zeros(graph_stride, np.uint32)
+        self.lib.ungo_pack_anchor_row(top, cand_degree, n, local_src, final_degree, head_keep,
+                                      anchor_tail, anchor_slots, bidir_anchor, graph_stride, row)
+        return row
+
+
+class RefOracle:
+    """The reference's own compiled distance + SearchQueue (oracle/_ref)."""
+
+    def __init__(self, path: str = REF_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (needs /root/reference; `make -C oracle ref`)")
+        L = C.CDLL(path)
+        L.ungref_l2.restype = C.c_float
+        L.ungref_l2.argtypes = [_f32p, _f32p, C.c_uint32]
+        L.ungref_queue_stream.restype = C.c_int32
+        L.ungref_queue_stream.argtypes = [_u32p, _f32p, C.c_uint32, C.c_int32, _u32p, _f32p]
+        L.ungref_cross_exact.restype = None
+        L.ungref_cross_exact.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, _u32p, _u32p,
+                                         _u32p, C.c_uint32, _u32p, _f32p, _i32p, C.c_int]
+        L.ungref_cross_exact_points.restype = None
+        L.ungref_cross_exact_points.argtypes = [_f32p, C.c_uint32, _u32p, _u32p, _u32p, _u32p,
+                                                _u32p, C.c_uint32, C.c_uint32, _u32p, _f32p, C.c_int]
+        L.ungref_intra_exact.restype = None
+        L.ungref_intra_exact.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                         _u32p, _f32p, C.c_int]
+        self.lib = L
+
+    def l2(self, a, b) -> float:
+        a, b = _f32(a), _f32(b)
+        return float(self.lib.ungref_l2(a, b, a.shape[0]))
+
+    def queue_stream(self, ids, dists, cap):
+        ids, dists = _u32(ids), _f32(dists)
+        oi = np.zeros(max(cap, 1), np.uint32)
+        od = np.zeros(max(cap, 1), np.float32)
+        n = self.lib.ungref_queue_stream(ids, dists, ids.shape[0], cap, oi, od)
+        return oi[:n].copy(), od[:n].copy()
+
+    def cross_exact(self, X, group_begin, in_ptr, in_idx, k, nthreads=0):
+        X = _f32(X)
+        N, d = X.shape
+        G = group_begin.shape[0] - 2
+        ids = np.zeros((N, k), np.uint32)
+        dists = np.zeros((N, k), np.float32)
+        size = np.zeros(N, np.int32)
+        in_idx = _u32(in_idx) if len(in_idx) else np.zeros(1, np.uint32)
+        self.lib.ungref_cross_exact(X, N, d, G, _u32(group_begin), _u32(in_ptr), in_idx,
+                                    k, ids, dists, size, nthreads)
+        return ids, dists, size
+
+    def cross_exact_points(self, X, group_begin, point_group, out_ptr, out_idx, q_list, k, nthreads=0):
+        X = _f32(X)
+        q_list = _u32(q_list)
+        nq = q_list.shape[0]
+        ids = np.zeros((nq, k), np.uint32)
+        dists = np.zeros((nq, k), np.float32)
+        out_idx = _u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
+        self.lib.ungref_cross_exact_points(X, X.shape[1], _u32(group_begin), _u32(point_group),
+                                           _u32(out_ptr), out_idx, q_list, nq, k, ids, dists,
+                                           nthreads)
+        return ids, dists
+
+    def intra_exact(self, X, begin, n, K, nthreads=0):
+        X = _f32(X)
+        ids = np.zeros((n, K), np.uint32)
+        dists = np.zeros((n, K), np.float32)
+        self.lib.ungref_intra_exact(X, X.shape[1], begin, n, K, ids, dists, nthreads)
+        return ids, dists
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)

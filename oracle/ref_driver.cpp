@@ -1,0 +1,172 @@
+// ref_driver.cpp -- thin C entry points around the reference's OWN compiled
+// FloatL2DistanceHandler (UNG/codes/src/distance.cpp) and SearchQueue
+// (UNG/codes/src/search_queue.cpp), built into oracle/_ref/libungref.so by
+// oracle/Makefile directly from /root/reference (nothing copied into this repo).
+//
+// TEST INFRASTRUCTURE ONLY: used to pin the plain-C oracle (oracle/ung_oracle.c),
+// to write tests/golden fixtures, and as the "reference" CPU baseline in bench.py.
+//
+// The two loops below restate the reference's CPU exact builders around those
+// compiled objects:
+//   ungref_cross_exact  -> UniNavGraph::build_cross_edges_generate_cpu_exact_scan
+//                          + append_cross_edges_from_target_range
+//                          (src/uni_nav_graph_cross_edges.cpp:154-220, :32-57)
+//   ungref_intra_exact  -> build_exact_topk_graph_for_points
+//                          (src/uni_nav_graph_special_blocks.cpp:70-111)
+// (their host file needs Boost and cannot be compiled here).
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <limits>
+#include <utility>
+#include <vector>
+#include <omp.h>
+
+#include "distance.h"
+#include "search_queue.h"
+
+using ANNS::FloatL2DistanceHandler;
+using ANNS::SearchQueue;
+
+extern "C" {
+
+float ungref_l2(const float *a, const float *b, uint32_t dim)
+{
+    static const FloatL2DistanceHandler h;
+    return h.compute(reinterpret_cast<const char *>(a), reinterpret_cast<const char *>(b), dim);
+}
+
+// Feed a stream of (id, dist) into one SearchQueue of capacity cap and return
+// its final content (size returned).
+int32_t ungref_queue_stream(const uint32_t *ids, const float *dists, uint32_t n, int32_t cap,
+                            uint32_t *out_ids, float *out_dists)
+{
+    SearchQueue q;
+    q.reserve(cap);
+    for (uint32_t i = 0; i < n; ++i)
+        q.insert(ids[i], dists[i]);
+    for (int32_t j = 0; j < q.size(); ++j) {
+        out_ids[j] = q[j].id;
+        out_dists[j] = q[j].distance;
+    }
+    return q.size();
+}
+
+void ungref_cross_exact(const float *X, uint32_t N, uint32_t dim, uint32_t G,
+                        const uint32_t *group_begin, const uint32_t *in_ptr, const uint32_t *in_idx,
+                        uint32_t k, uint32_t *out_ids, float *out_dists, int32_t *out_size,
+                        int nthreads)
+{
+    const FloatL2DistanceHandler h;
+    std::vector<SearchQueue> queues(N);
+    for (uint32_t i = 0; i < N; ++i)
+        queues[i].reserve((int32_t)k);
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+    for (uint32_t x = 1; x <= G; ++x) {
+        if (in_ptr[x + 1] == in_ptr[x])
+            continue;
+        const uint32_t xf = group_begin[x], xs = group_begin[x + 1];
+        if (xs == xf)
+            continue;
+        for (uint32_t e = in_ptr[x]; e < in_ptr[x + 1]; ++e) {
+            const uint32_t c = in_idx[e];
+            const int64_t qf = group_begin[c], qs = group_begin[c + 1];
+#pragma omp parallel for schedule(dynamic, 1)
+            for (int64_t q = qf; q < qs; ++q) {
+                SearchQueue local;
+                local.reserve((int32_t)k);
+                const char *qv = reinterpret_cast<const char *>(X + (size_t)q * dim);
+                for (uint32_t t = xf; t < xs; ++t)
+                    local.insert(t, h.compute(qv, reinterpret_cast<const char *>(X + (size_t)t * dim), dim));
+                for (int j = 0; j < local.size(); ++j)
+                    queues[q].insert(local[j].id, local[j].distance);
+            }
+        }
+    }
+    for (uint32_t i = 0; i < N; ++i) {
+        out_size[i] = queues[i].size();
+        for (uint32_t j = 0; j < k; ++j) {
+            const bool has = (int32_t)j < queues[i].size();
+            out_ids[(size_t)i * k + j] = has ? queues[i][j].id : UINT32_MAX;
+            out_dists[(size_t)i * k + j] = has ? queues[i][j].distance : INFINITY;
+        }
+    }
+}
+
+// Bounded sample of the cross-edge exact scan for listed query points (used for
+// the timed CPU baseline): same per-(target, query) local queue + merge, with
+// the targets of a point's group given as an out-neighbour CSR.
+void ungref_cross_exact_points(const float *X, uint32_t dim, const uint32_t *group_begin,
+                               const uint32_t *point_group, const uint32_t *out_ptr,
+                               const uint32_t *out_idx, const uint32_t *q_list, uint32_t n_q,
+                               uint32_t k, uint32_t *out_ids, float *out_dists, int nthreads)
+{
+    const FloatL2DistanceHandler h;
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t i = 0; i < (int64_t)n_q; ++i) {
+        const uint32_t q = q_list[i];
+        SearchQueue acc;
+        acc.reserve((int32_t)k);
+        const char *qv = reinterpret_cast<const char *>(X + (size_t)q * dim);
+        const uint32_t c = point_group[q];
+        for (uint32_t e = out_ptr[c]; e < out_ptr[c + 1]; ++e) {
+            const uint32_t x = out_idx[e];
+            SearchQueue local;
+            local.reserve((int32_t)k);
+            for (uint32_t t = group_begin[x]; t < group_begin[x + 1]; ++t)
+                local.insert(t, h.compute(qv, reinterpret_cast<const char *>(X + (size_t)t * dim), dim));
+            for (int j = 0; j < local.size(); ++j)
+                acc.insert(local[j].id, local[j].distance);
+        }
+        for (uint32_t j = 0; j < k; ++j) {
+            const bool has = (int32_t)j < acc.size();
+            out_ids[(size_t)i * k + j] = has ? acc[j].id : UINT32_MAX;
+            out_dists[(size_t)i * k + j] = has ? acc[j].distance : INFINITY;
+        }
+    }
+}
+
+void ungref_intra_exact(const float *X, uint32_t dim, uint32_t begin, uint32_t n, uint32_t K,
+                        uint32_t *out_ids, float *out_dists, int nthreads)
+{
+    const FloatL2DistanceHandler h;
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+    const uint32_t degree = n > 0 ? std::min<uint32_t>(K, n - 1) : 0;
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t i = 0; i < (int64_t)n; ++i) {
+        uint32_t *ids = out_ids + (size_t)i * K;
+        float *ds = out_dists + (size_t)i * K;
+        for (uint32_t j = 0; j < K; ++j) {
+            ids[j] = UINT32_MAX;
+            ds[j] = INFINITY;
+        }
+        if (n <= 1)
+            continue;
+        std::vector<std::pair<float, uint32_t>> cand;
+        cand.reserve(n - 1);
+        const char *src = reinterpret_cast<const char *>(X + ((size_t)begin + i) * dim);
+        for (uint32_t j = 0; j < n; ++j) {
+            if (j == (uint32_t)i)
+                continue;
+            cand.emplace_back(h.compute(src, reinterpret_cast<const char *>(X + ((size_t)begin + j) * dim), dim), j);
+        }
+        auto less = [](const std::pair<float, uint32_t> &a, const std::pair<float, uint32_t> &b) {
+            return a.first < b.first || (a.first == b.first && a.second < b.second);
+        };
+        if (cand.size() > degree) {
+            std::nth_element(cand.begin(), cand.begin() + degree, cand.end(), less);
+            cand.resize(degree);
+        }
+        std::sort(cand.begin(), cand.end(), less);
+        for (size_t j = 0; j < cand.size(); ++j) {
+            ids[j] = cand[j].second;
+            ds[j] = cand[j].first;
+        }
+    }
+}
+
+} // extern "C"

@@ -1,0 +1,465 @@
+/*
+ * ung_oracle.c -- CPU oracle for the UNG cross-edge / mid-group kNN build stage.
+ *
+ * TEST INFRASTRUCTURE ONLY (see ung_oracle.h): loaded by tests/, by
+ * __graft_entry__.smoke() and by the cpu_baseline leg of bench.py, never by the
+ * product.  Plain C restatement of the reference's CPU semantics; every
+ * function names the reference file:line it follows (paths under UNG/codes/).
+ *
+ * Build: oracle/Makefile (gcc -O3 -fopenmp -ffp-contract=off; fmaf() is the
+ * only fused operation, written out where the reference's release build fuses).
+ *
+ * Parity pins (tests/test_oracle.py):
+ *   ungo_l2            bit-exact vs the reference's own distance.cpp compiled
+ *                      under oracle/_ref with its release flags, and within
+ *                      fp32 error bounds of a float64 brute force;
+ *   ungo_queue_insert  element-wise vs the reference's compiled SearchQueue
+ *                      (oracle/_ref) on random insert streams, and vs sorting;
+ *   ungo_cross_exact   vs committed golden fixtures made by oracle/_ref and
+ *                      vs a float64 brute-force top-k outside the tie band;
+ *   ungo_intra_exact   vs oracle/_ref fixtures and a float64 brute force;
+ *   ungo_divide_groups vs a Python dict-based first-appearance grouping;
+ *   ungo_min_supersets vs a Python itertools enumeration of the definition;
+ *   ungo_pack_anchor_row  vs hand-worked rows (small n) and invariants.
+ */
+#include "ung_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* src/distance.cpp:34-91 (release build: the _mm256_add_ps(acc, _mm256_mul_ps(d,d))
+ * pair is contracted to one vfmadd231ps; verified against the compiled reference). */
+float ungo_l2(const float *a, const float *b, uint32_t dim)
+{
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t p = 0;
+    while (dim - p >= 8) {
+        for (int l = 0; l < 8; ++l) {
+            const float d = a[p + l] - b[p + l];
+            acc[l] = fmaf(d, d, acc[l]);
+        }
+        p += 8;
+    }
+    float s[4];
+    for (int i = 0; i < 4; ++i)
+        s[i] = acc[i + 4] + acc[i];
+    uint32_t rem = dim - p;
+    if (rem >= 4) {
+        for (int i = 0; i < 4; ++i) {
+            const float d = a[p + i] - b[p + i];
+            s[i] = fmaf(d, d, s[i]);
+        }
+        p += 4;
+        rem -= 4;
+    }
+    for (uint32_t i = 0; i < rem; ++i) {
+        const float d = a[p + i] - b[p + i];
+        s[i] = fmaf(d, d, s[i]);
+    }
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+double ungo_l2_f64(const float *a, const float *b, uint32_t dim)
+{
+    double s = 0.0;
+    for (uint32_t i = 0; i < dim; ++i) {
+        const double d = (double)a[i] - (double)b[i];
+        s += d * d;
+    }
+    return s;
+}
+
+static inline int cand_less(float da, uint32_t ia, float db, uint32_t ib)
+{
+    return da < db || (da == db && ia < ib);
+}
+
+/* src/search_queue.cpp:26-53 */
+int ungo_queue_insert(uint32_t *ids, float *dists, int32_t *size, int32_t cap,
+                      uint32_t id, float dist)
+{
+    int32_t n = *size;
+    if (cap <= 0)
+        return -1;
+    if (n == cap && cand_less(dists[n - 1], ids[n - 1], dist, id))
+        return -1;
+    int32_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (cand_less(dist, id, dists[mid], ids[mid]))
+            hi = mid;
+        else if (ids[mid] == id)
+            return -1;
+        else
+            lo = mid + 1;
+    }
+    /* the reference keeps capacity+1 slots and lets the tail fall off */
+    int32_t last = (n < cap) ? n : cap - 1;
+    for (int32_t j = last; j > lo; --j) {
+        ids[j] = ids[j - 1];
+        dists[j] = dists[j - 1];
+    }
+    if (lo < cap) {
+        ids[lo] = id;
+        dists[lo] = dist;
+    }
+    if (n < cap)
+        *size = n + 1;
+    return lo < cap ? lo : -1;
+}
+
+/* ---- group division (label_graph.cpp:21-43, trie.cpp:23-55, uni_nav_graph.cpp:148-166) ---- */
+
+typedef struct {
+    const uint32_t *lab_ptr;
+    const uint32_t *lab_idx;
+} label_ctx;
+
+static const label_ctx *g_sort_ctx;
+
+static int cmp_label_rows(uint32_t a, uint32_t b, const label_ctx *c)
+{
+    uint32_t la = c->lab_ptr[a + 1] - c->lab_ptr[a];
+    uint32_t lb = c->lab_ptr[b + 1] - c->lab_ptr[b];
+    const uint32_t *pa = c->lab_idx + c->lab_ptr[a];
+    const uint32_t *pb = c->lab_idx + c->lab_ptr[b];
+    uint32_t m = la < lb ? la : lb;
+    for (uint32_t i = 0; i < m; ++i) {
+        if (pa[i] != pb[i])
+            return pa[i] < pb[i] ? -1 : 1;
+    }
+    if (la != lb)
+        return la < lb ? -1 : 1;
+    return 0;
+}
+
+static int cmp_points(const void *x, const void *y)
+{
+    uint32_t a = *(const uint32_t *)x, b = *(const uint32_t *)y;
+    int c = cmp_label_rows(a, b, g_sort_ctx);
+    if (c)
+        return c;
+    return a < b ? -1 : (a > b);
+}
+
+typedef struct {
+    uint32_t first_point;
+    uint32_t rank; /* index into the sorted distinct list */
+} first_seen;
+
+static int cmp_first(const void *x, const void *y)
+{
+    const first_seen *a = (const first_seen *)x, *b = (const first_seen *)y;
+    return a->first_point < b->first_point ? -1 : (a->first_point > b->first_point);
+}
+
+uint32_t ungo_divide_groups(uint32_t n, const uint32_t *lab_ptr, const uint32_t *lab_idx,
+                            uint32_t *point_group, uint32_t *group_begin, uint32_t *new_to_old)
+{
+    if (n == 0) {
+        group_begin[0] = 0;
+        group_begin[1] = 0;
+        return 0;
+    }
+    label_ctx ctx = {lab_ptr, lab_idx};
+    uint32_t *order = (uint32_t *)malloc(sizeof(uint32_t) * n);
+    for (uint32_t i = 0; i < n; ++i)
+        order[i] = i;
+    g_sort_ctx = &ctx;
+    qsort(order, n, sizeof(uint32_t), cmp_points);
+    /* distinct label sets; within one set `order` is ascending point id, so the
+     * first element is the first appearance */
+    first_seen *fs = (first_seen *)malloc(sizeof(first_seen) * n);
+    uint32_t *rank_of_sorted = (uint32_t *)malloc(sizeof(uint32_t) * n);
+    uint32_t nd = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        if (i == 0 || cmp_label_rows(order[i - 1], order[i], &ctx) != 0) {
+            fs[nd].first_point = order[i];
+            fs[nd].rank = nd;
+            ++nd;
+        }
+        rank_of_sorted[i] = nd - 1;
+    }
+    qsort(fs, nd, sizeof(first_seen), cmp_first);
+    uint32_t *gid_of_rank = (uint32_t *)malloc(sizeof(uint32_t) * nd);
+    for (uint32_t g = 0; g < nd; ++g)
+        gid_of_rank[fs[g].rank] = g + 1; /* group ids 1..G in first-appearance order */
+    for (uint32_t i = 0; i < n; ++i)
+        point_group[order[i]] = gid_of_rank[rank_of_sorted[i]];
+    /* reorder: groups 1..G, original ascending order inside a group */
+    uint32_t *count = (uint32_t *)calloc(nd + 2, sizeof(uint32_t));
+    for (uint32_t i = 0; i < n; ++i)
+        count[point_group[i]]++;
+    group_begin[0] = 0;
+    group_begin[1] = 0;
+    for (uint32_t g = 1; g <= nd; ++g)
+        group_begin[g + 1] = group_begin[g] + count[g];
+    uint32_t *fill = (uint32_t *)calloc(nd + 2, sizeof(uint32_t));
+    for (uint32_t i = 0; i < n; ++i) {
+        uint32_t g = point_group[i];
+        new_to_old[group_begin[g] + fill[g]++] = i;
+    }
+    free(fill);
+    free(count);
+    free(gid_of_rank);
+    free(rank_of_sorted);
+    free(fs);
+    free(order);
+    return nd;
+}
+
+/* ---- minimum proper supersets by definition ---- */
+
+static int is_subset(const uint32_t *a, uint32_t la, const uint32_t *b, uint32_t lb)
+{
+    /* a subset-of b, both sorted ascending (std::includes semantics) */
+    uint32_t i = 0, j = 0;
+    while (i < la) {
+        while (j < lb && b[j] < a[i])
+            ++j;
+        if (j == lb || b[j] != a[i])
+            return 0;
+        ++i;
+        ++j;
+    }
+    return 1;
+}
+
+int64_t ungo_min_supersets(uint32_t G, const uint32_t *set_ptr, const uint32_t *set_idx,
+                           uint32_t *out_ptr, uint32_t *out_idx, int64_t out_cap)
+{
+    int64_t total = 0;
+    uint32_t *sup = (uint32_t *)malloc(sizeof(uint32_t) * (G + 1));
+    out_ptr[0] = 0;
+    out_ptr[1] = 0;
+    for (uint32_t c = 1; c <= G; ++c) {
+        const uint32_t *sc = set_idx + set_ptr[c];
+        const uint32_t lc = set_ptr[c + 1] - set_ptr[c];
+        uint32_t ns = 0;
+        for (uint32_t x = 1; x <= G; ++x) {
+            const uint32_t lx = set_ptr[x + 1] - set_ptr[x];
+            if (x == c || lx <= lc)
+                continue;
+            if (is_subset(sc, lc, set_idx + set_ptr[x], lx))
+                sup[ns++] = x;
+        }
+        for (uint32_t i = 0; i < ns; ++i) {
+            const uint32_t x = sup[i];
+            const uint32_t lx = set_ptr[x + 1] - set_ptr[x];
+            int minimal = 1;
+            for (uint32_t j = 0; j < ns && minimal; ++j) {
+                const uint32_t y = sup[j];
+                const uint32_t ly = set_ptr[y + 1] - set_ptr[y];
+                if (y != x && ly < lx && is_subset(set_idx + set_ptr[y], ly, set_idx + set_ptr[x], lx))
+                    minimal = 0;
+            }
+            if (minimal) {
+                if (total >= out_cap) {
+                    free(sup);
+                    return -1;
+                }
+                out_idx[total++] = x;
+            }
+        }
+        out_ptr[c + 1] = (uint32_t)total;
+    }
+    free(sup);
+    return total;
+}
+
+/* ---- cross edges: uni_nav_graph_cross_edges.cpp:154-220 and :32-57 ---- */
+
+static void local_topk_over_range(const float *X, uint32_t dim, uint32_t q, uint32_t first,
+                                  uint32_t second, uint32_t k, uint32_t *lids, float *ldists,
+                                  uint32_t *qids, float *qdists, int32_t *qsize)
+{
+    int32_t lsize = 0;
+    const float *qv = X + (size_t)q * dim;
+    for (uint32_t t = first; t < second; ++t) {
+        const float d = ungo_l2(qv, X + (size_t)t * dim, dim);
+        ungo_queue_insert(lids, ldists, &lsize, (int32_t)k, t, d);
+    }
+    for (int32_t j = 0; j < lsize; ++j)
+        ungo_queue_insert(qids, qdists, qsize, (int32_t)k, lids[j], ldists[j]);
+}
+
+void ungo_cross_exact(const float *X, uint32_t N, uint32_t dim, uint32_t G,
+                      const uint32_t *group_begin, const uint32_t *in_ptr, const uint32_t *in_idx,
+                      uint32_t k, uint32_t *out_ids, float *out_dists, int32_t *out_size,
+                      int nthreads)
+{
+    for (size_t i = 0; i < (size_t)N * k; ++i) {
+        out_ids[i] = UINT32_MAX;
+        out_dists[i] = INFINITY;
+    }
+    for (uint32_t i = 0; i < N; ++i)
+        out_size[i] = 0;
+#ifdef _OPENMP
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+    for (uint32_t x = 1; x <= G; ++x) {
+        if (in_ptr[x + 1] == in_ptr[x])
+            continue;
+        const uint32_t xf = group_begin[x], xs = group_begin[x + 1];
+        if (xs == xf)
+            continue;
+        for (uint32_t e = in_ptr[x]; e < in_ptr[x + 1]; ++e) {
+            const uint32_t c = in_idx[e];
+            const int64_t qf = group_begin[c], qs = group_begin[c + 1];
+#pragma omp parallel
+            {
+                uint32_t *lids = (uint32_t *)malloc(sizeof(uint32_t) * (k + 1));
+                float *ld = (float *)malloc(sizeof(float) * (k + 1));
+#pragma omp for schedule(dynamic, 1)
+                for (int64_t q = qf; q < qs; ++q)
+                    local_topk_over_range(X, dim, (uint32_t)q, xf, xs, k, lids, ld,
+                                          out_ids + (size_t)q * k, out_dists + (size_t)q * k,
+                                          out_size + q);
+                free(lids);
+                free(ld);
+            }
+        }
+    }
+}
+
+void ungo_cross_exact_points(const float *X, uint32_t N, uint32_t dim, uint32_t G,
+                             const uint32_t *group_begin, const uint32_t *point_group,
+                             const uint32_t *out_ptr, const uint32_t *out_idx,
+                             const uint32_t *q_list, uint32_t n_q, uint32_t k,
+                             uint32_t *out_ids, float *out_dists, int32_t *out_size,
+                             int nthreads)
+{
+    (void)N;
+    (void)G;
+#ifdef _OPENMP
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+#pragma omp parallel
+    {
+        uint32_t *lids = (uint32_t *)malloc(sizeof(uint32_t) * (k + 1));
+        float *ld = (float *)malloc(sizeof(float) * (k + 1));
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t i = 0; i < (int64_t)n_q; ++i) {
+            const uint32_t q = q_list[i];
+            uint32_t *qi = out_ids + (size_t)i * k;
+            float *qd = out_dists + (size_t)i * k;
+            for (uint32_t j = 0; j < k; ++j) {
+                qi[j] = UINT32_MAX;
+                qd[j] = INFINITY;
+            }
+            out_size[i] = 0;
+            const uint32_t c = point_group[q];
+            for (uint32_t e = out_ptr[c]; e < out_ptr[c + 1]; ++e) {
+                const uint32_t x = out_idx[e];
+                local_topk_over_range(X, dim, q, group_begin[x], group_begin[x + 1], k, lids, ld,
+                                      qi, qd, out_size + i);
+            }
+        }
+        free(lids);
+        free(ld);
+    }
+}
+
+/* ---- intra-group exact top-K: uni_nav_graph_special_blocks.cpp:70-111 ---- */
+
+void ungo_intra_exact(const float *X, uint32_t dim, uint32_t begin, uint32_t n, uint32_t K,
+                      uint32_t *out_ids, float *out_dists, int nthreads)
+{
+#ifdef _OPENMP
+    if (nthreads > 0)
+        omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+    const uint32_t degree = (n > 0) ? (K < n - 1 ? K : n - 1) : 0;
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t i = 0; i < (int64_t)n; ++i) {
+        uint32_t *ids = out_ids + (size_t)i * K;
+        float *ds = out_dists + (size_t)i * K;
+        for (uint32_t j = 0; j < K; ++j) {
+            ids[j] = UINT32_MAX;
+            ds[j] = INFINITY;
+        }
+        if (degree == 0)
+            continue;
+        int32_t size = 0;
+        const float *src = X + ((size_t)begin + (size_t)i) * dim;
+        /* (dist, local j) is a total order over distinct j, so keeping the
+         * `degree` smallest while scanning equals nth_element + sort */
+        for (uint32_t j = 0; j < n; ++j) {
+            if (j == (uint32_t)i)
+                continue;
+            const float d = ungo_l2(src, X + ((size_t)begin + j) * dim, dim);
+            ungo_queue_insert(ids, ds, &size, (int32_t)degree, j, d);
+        }
+    }
+}
+
+/* ---- exact-anchor packing: tagore_graph_builder.cu:727-794 ---- */
+
+static int row_has(const uint32_t *row, uint32_t write, uint32_t v)
+{
+    for (uint32_t p = 0; p < write; ++p)
+        if (row[1 + p] == v)
+            return 1;
+    return 0;
+}
+
+void ungo_pack_anchor_row(const uint32_t *top_idx, uint32_t cand_degree, uint32_t n,
+                          uint32_t local_src, uint32_t final_degree, uint32_t head_keep,
+                          uint32_t anchor_tail, uint32_t anchor_slots, uint32_t bidir_anchor,
+                          uint32_t graph_stride, uint32_t *row)
+{
+    const uint32_t out_degree = final_degree < cand_degree ? final_degree : cand_degree;
+    row[0] = out_degree;
+    if (out_degree > 0) {
+        uint32_t near_limit = head_keep < final_degree ? head_keep : final_degree;
+        if (out_degree < near_limit)
+            near_limit = out_degree;
+        uint32_t write = 0;
+        for (; write < near_limit; ++write)
+            row[1 + write] = top_idx[write];
+        const uint32_t remaining = final_degree > write ? final_degree - write : 0;
+        uint32_t anchor_limit = 0;
+        if (anchor_tail)
+            anchor_limit = (anchor_slots == 0) ? remaining : (anchor_slots < remaining ? anchor_slots : remaining);
+        if (anchor_limit > 0 && n > 1) {
+            for (uint32_t t = 0; t < anchor_limit && write < out_degree; ++t) {
+                uint32_t hop = ((t + 1) * n) / (anchor_limit + 1);
+                if (hop < 1)
+                    hop = 1;
+                const int backward = bidir_anchor && (t & 1u);
+                uint32_t cand = backward ? (local_src + n - (hop % n)) % n : (local_src + hop) % n;
+                for (uint32_t retry = 0; retry < n && write < out_degree; ++retry) {
+                    if (cand != local_src && !row_has(row, write, cand)) {
+                        row[1 + write++] = cand;
+                        break;
+                    }
+                    cand = backward ? (cand + n - 1) % n : (cand + 1) % n;
+                }
+            }
+        }
+        const uint32_t tail_start = near_limit;
+        const uint32_t tail_count = cand_degree > tail_start ? cand_degree - tail_start : 0;
+        const uint32_t step = (tail_count > remaining && remaining > 0)
+                                  ? (tail_count + remaining - 1) / remaining
+                                  : 1;
+        for (uint32_t s = tail_start; s < cand_degree && write < out_degree; s += step)
+            row[1 + write++] = top_idx[s];
+        for (uint32_t s = tail_start; s < cand_degree && write < out_degree; ++s)
+            if (!row_has(row, write, top_idx[s]))
+                row[1 + write++] = top_idx[s];
+    }
+    for (uint32_t j = out_degree; j + 1 < graph_stride; ++j)
+        row[1 + j] = local_src;
+}

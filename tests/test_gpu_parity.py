@@ -1,0 +1,200 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Bar: ids bit-exact and fp32 distances bit-exact (the exact re-rank reproduces
+the reference's summation order), sizes exact.  Every call goes through the C ABI
+(libung_hip.so via ctypes).
+"""
+import numpy as np
+import pytest
+
+import filtervectorcode_refactor_amd as F
+from filtervectorcode_refactor_amd import datasets as D
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = F.HipContext(0)
+    yield c
+    c.close()
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _assert_rows_equal(ids_g, dist_g, size_g, ids_o, dist_o, size_o, what):
+    assert ids_g.shape == ids_o.shape, what
+    bad = np.nonzero((ids_g != ids_o).any(axis=1))[0]
+    assert bad.size == 0, f"{what}: {bad.size} rows differ in ids, first {bad[:5]}: gpu {ids_g[bad[0]]} oracle {ids_o[bad[0]]} d_gpu {dist_g[bad[0]]} d_or {dist_o[bad[0]]}"
+    assert np.array_equal(dist_g.view(np.uint32), dist_o.view(np.uint32)), f"{what}: distances not bit-exact"
+    if size_g is not None:
+        assert np.array_equal(size_g, size_o), f"{what}: sizes differ"
+
+
+def test_mfma_layout(ctx):
+    _say("test_mfma_layout")
+    assert ctx.selftest_mfma() == 0.0
+
+
+def test_cross_cfg1_bitexact(ctx, cfg1_stage, oracle):
+    st = cfg1_stage
+    _say("cross cfg1: prepare")
+    ctx.prepare_vectors(st.base)
+    ids, dist, size, stats = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+    _say(f"cross cfg1 stats {stats}")
+    oi, od, os_ = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    _assert_rows_equal(ids, dist, size, oi, od, os_, "cfg1 cross k=6")
+    assert stats["pairs"] == F.count_pairs(st.group_begin, st.out_ptr, st.out_idx)[0]
+
+
+def test_intra_cfg1_bitexact(ctx, cfg1_stage, oracle):
+    st = cfg1_stage
+    ctx.prepare_vectors(st.base)
+    gids = st.mid_groups()
+    assert len(gids) > 0
+    begins = st.group_begin[gids]
+    sizes = st.group_begin[gids + 1] - begins
+    _say(f"intra cfg1: {len(gids)} groups, sizes {sizes.min()}..{sizes.max()}")
+    ids, dist, stats = ctx.group_knn(begins, sizes, 32)
+    _say(f"intra cfg1 stats {stats}")
+    row = 0
+    for b, n in zip(begins, sizes):
+        oi, od = oracle.intra_exact(st.base, int(b), int(n), 32)
+        _assert_rows_equal(ids[row: row + n], dist[row: row + n], None, oi, od, None, f"intra group@{b} n={n}")
+        row += n
+
+
+def test_pack_cfg1_matches_oracle(ctx, cfg1_stage, oracle):
+    st = cfg1_stage
+    ctx.prepare_vectors(st.base)
+    gids = st.mid_groups()
+    begins = st.group_begin[gids]
+    sizes = st.group_begin[gids + 1] - begins
+    for list_k, anchor_tail in ((32, 1), (63, 0)):
+        ids, dist, _ = ctx.group_knn(begins, sizes, list_k)
+        graph, entries, _ = ctx.pack_anchor_rows(ids.shape[0], len(gids), 64, 32, 24, anchor_tail, 0, 0)
+        row = 0
+        for b, n in zip(begins, sizes):
+            cand = min(64, 63, int(n) - 1)
+            for j in range(int(n)):
+                ref = oracle.pack_anchor_row(ids[row + j][:cand] if cand <= list_k else ids[row + j], cand, int(n), j,
+                                             32, 24, anchor_tail, 0, 0, 33)
+                assert np.array_equal(graph[row + j], ref), (list_k, anchor_tail, b, j)
+            row += n
+        assert (entries == 0).all()
+
+
+def _two_level_problem(rng, sizes_children, sizes_targets, dim, dup=False):
+    """Children 1..C, targets C+1..C+T; every child points to a random subset of
+    targets (possibly none).  Returns X (group-contiguous), group_begin, out CSR."""
+    C = len(sizes_children)
+    sizes = list(sizes_children) + list(sizes_targets)
+    G = len(sizes)
+    gb = np.zeros(G + 2, np.uint32)
+    gb[2:] = np.cumsum(sizes)
+    N = int(gb[-1])
+    X = rng.standard_normal((N, dim)).astype(np.float32)
+    if dup:
+        # exact duplicates across groups -> equal distances, ties broken by id
+        X[gb[C + 1]: gb[C + 1] + 3] = X[gb[1]: gb[1] + 3]
+        X[gb[G]: gb[G] + 2] = X[gb[C + 1]: gb[C + 1] + 2]
+    out_ptr = np.zeros(G + 2, np.uint32)
+    rows = []
+    for c in range(1, G + 1):
+        if c <= C:
+            m = rng.integers(0, len(sizes_targets) + 1)
+            row = sorted(rng.choice(np.arange(C + 1, G + 1), size=m, replace=False).tolist())
+        else:
+            row = []
+        rows.append(row)
+        out_ptr[c + 1] = out_ptr[c] + len(row)
+    out_idx = np.array([v for r in rows for v in r], np.uint32)
+    return X, gb, out_ptr, out_idx
+
+
+@pytest.mark.parametrize("dim,k,seed", [(128, 6, 1), (37, 6, 2), (12, 1, 3), (64, 64, 4), (128, 20, 5),
+                                        (768, 6, 6), (5, 6, 7)])
+def test_cross_edge_cases(ctx, oracle, dim, k, seed):
+    rng = np.random.default_rng(seed)
+    _say(f"cross edge case dim={dim} k={k}")
+    X, gb, op, oi = _two_level_problem(rng, [1, 2, 3, 130, 300, 7, 1], [1, 4, 200, 2, 129, 5], dim, dup=(seed == 1))
+    ctx.prepare_vectors(X)
+    ids, dist, size, stats = ctx.cross_topk(gb, op, oi, k)
+    ip, ii = F.in_neighbors(op, oi)
+    o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, k)
+    _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, f"edge dim={dim} k={k}")
+
+
+def test_cross_multi_split(ctx, oracle):
+    """Unions above one work item's candidate split (16384) are merged on device."""
+    rng = np.random.default_rng(11)
+    X, gb, op, oi = _two_level_problem(rng, [300, 5], [9000, 12000, 3], 128)
+    op = np.array([0, 0, 3, 6, 6, 6, 6], np.uint32)
+    oi = np.array([3, 4, 5, 3, 4, 5], np.uint32)
+    ctx.prepare_vectors(X)
+    ids, dist, size, stats = ctx.cross_topk(gb, op, oi, 6)
+    _say(f"multi split stats {stats}")
+    ip, ii = F.in_neighbors(op, oi)
+    o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, 6)
+    _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, "multi split")
+
+
+@pytest.mark.parametrize("n,list_k,dim", [(2, 32, 128), (3, 1, 16), (129, 32, 128), (200, 64, 40), (700, 32, 384),
+                                          (20000, 8, 64)])
+def test_intra_edge_cases(ctx, oracle, n, list_k, dim):
+    rng = np.random.default_rng(n)
+    _say(f"intra edge case n={n} k={list_k} dim={dim}")
+    X = rng.standard_normal((n + 10, dim)).astype(np.float32)
+    if n > 5:
+        X[6] = X[2]  # duplicate inside the group: equal distances, (dist, id) order
+    ctx.prepare_vectors(X)
+    ids, dist, stats = ctx.group_knn([5], [n], list_k)
+    oi, od = oracle.intra_exact(X, 5, n, list_k)
+    _assert_rows_equal(ids, dist, None, oi, od, None, f"intra n={n}")
+
+
+def test_errors(ctx):
+    X = np.zeros((10, 8), np.float32)
+    ctx.prepare_vectors(X)
+    gb = np.array([0, 0, 5, 10], np.uint32)
+    op = np.array([0, 0, 1, 1], np.uint32)
+    oi = np.array([2], np.uint32)
+    with pytest.raises(F.UngHipError) as e:
+        ctx.cross_topk(gb, op, oi, 0)
+    assert e.value.code == -1
+    with pytest.raises(F.UngHipError):
+        ctx.cross_topk(gb, op, oi, 65)
+    with pytest.raises(F.UngHipError):
+        ctx.cross_topk(np.array([0, 0, 5, 9], np.uint32), op, oi, 6)  # N mismatch
+    with pytest.raises(F.UngHipError):
+        ctx.group_knn([8], [5], 4)  # out of range
+    ctx.release_vectors()
+    with pytest.raises(F.UngHipError) as e:
+        ctx.cross_topk(gb, op, oi, 6)
+    assert e.value.code == -3
+
+
+def test_cfg2_scaled_parity(ctx, oracle):
+    """cfg2's generator at 60k points: cross + intra, bit-exact."""
+    cfg = D.scaled(D.CONFIGS["cfg2"], 60_000)
+    X, lp, li = D.generate(cfg)
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    ctx.prepare_vectors(st.base)
+    _say("cfg2@60k cross")
+    ids, dist, size, stats = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+    _say(f"stats {stats}")
+    oi, od, os_ = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    _assert_rows_equal(ids, dist, size, oi, od, os_, "cfg2@60k cross")
+    gids = st.mid_groups()
+    begins = st.group_begin[gids]
+    sizes = st.group_begin[gids + 1] - begins
+    _say(f"cfg2@60k intra {len(gids)} groups")
+    ids, dist, stats = ctx.group_knn(begins, sizes, 32)
+    row = 0
+    for b, n in zip(begins, sizes):
+        o_i, o_d = oracle.intra_exact(st.base, int(b), int(n), 32)
+        _assert_rows_equal(ids[row: row + n], dist[row: row + n], None, o_i, o_d, None, f"cfg2@60k intra {b}")
+        row += n
