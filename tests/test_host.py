@@ -1,0 +1,147 @@
+"""Host-side inputs of the path (C++ in libung_hip.so) against the oracle and
+closed forms: group division, reorder, label navigating graph, pair counts,
+synthetic generator, file formats.  CPU only."""
+import hashlib
+import itertools
+import os
+
+import numpy as np
+import pytest
+
+import filtervectorcode_refactor_amd as F
+from filtervectorcode_refactor_amd import datasets as D
+from conftest import load_golden
+
+
+def _labels(rng, n, vocab, mmax, lo=0, label_offset=0):
+    rows = []
+    for _ in range(n):
+        m = int(rng.integers(lo, mmax + 1))
+        rows.append(sorted((rng.choice(np.arange(1, vocab + 1), size=m, replace=False) + label_offset).tolist()))
+    lp = np.zeros(n + 1, np.uint32)
+    lp[1:] = np.cumsum([len(r) for r in rows])
+    li = np.array([v for r in rows for v in r], np.uint32)
+    return rows, lp, li
+
+
+@pytest.mark.parametrize("seed,vocab,mmax,lo", [(1, 5, 3, 0), (2, 12, 4, 1), (3, 30, 6, 1)])
+def test_divide_groups_matches_oracle(oracle, seed, vocab, mmax, lo):
+    rng = np.random.default_rng(seed)
+    _, lp, li = _labels(rng, 5000, vocab, mmax, lo)
+    a = F.divide_groups(lp, li)
+    b = oracle.divide_groups(lp, li)
+    assert a[0] == b[0]
+    for x, y in zip(a[1:], b[1:]):
+        assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("seed,vocab,mmax,offset", [(4, 6, 3, 0), (5, 10, 4, 0), (6, 9, 5, 5000)])
+def test_lng_matches_oracle(oracle, seed, vocab, mmax, offset):
+    """offset=5000 pushes label ids past the bitset path (sorted-merge subset test)."""
+    rng = np.random.default_rng(seed)
+    _, lp, li = _labels(rng, 4000, vocab, mmax, 0, offset)
+    G, pg, gb, n2o = F.divide_groups(lp, li)
+    sp, si = F.group_label_sets(lp, li, gb, n2o, G)
+    op, oi = F.lng_build(sp, si, nthreads=4)
+    rop, roi = oracle.min_supersets(sp, si)
+    assert np.array_equal(op, rop) and np.array_equal(oi, roi)
+
+
+def test_lng_definition_small():
+    """Every subset family of {1..4}: LNG rows equal the minimal-superset definition."""
+    universe = [list(s) for m in range(0, 5) for s in itertools.combinations(range(1, 5), m)]
+    rng = np.random.default_rng(0)
+    for _ in range(20):
+        pick = rng.choice(len(universe), size=int(rng.integers(2, len(universe))), replace=False)
+        sets = [universe[i] for i in pick]
+        sp = np.zeros(len(sets) + 2, np.uint32)
+        sp[2:] = np.cumsum([len(s) for s in sets])
+        si = np.array([v for s in sets for v in s], np.uint32)
+        op, oi = F.lng_build(sp, si, nthreads=2)
+        for c, s in enumerate(sets, start=1):
+            sup = [x for x, t in enumerate(sets, start=1) if set(s) < set(t)]
+            mins = sorted(x for x in sup if not any(set(sets[y - 1]) < set(sets[x - 1]) for y in sup))
+            assert oi[op[c]: op[c + 1]].tolist() == mins
+
+
+def test_in_neighbors_transpose():
+    op = np.array([0, 0, 2, 3, 3, 4], np.uint32)
+    oi = np.array([2, 3, 3, 1], np.uint32)
+    ip, ii = F.in_neighbors(op, oi)
+    rows = {x: ii[ip[x]: ip[x + 1]].tolist() for x in range(1, 5)}
+    assert rows == {1: [4], 2: [1], 3: [1, 2], 4: []}
+
+
+def test_reorder_rows():
+    rng = np.random.default_rng(1)
+    X = rng.standard_normal((1000, 37)).astype(np.float32)
+    p = rng.permutation(1000).astype(np.uint32)
+    assert np.array_equal(F.reorder_rows(X, p, 3), X[p])
+
+
+def test_count_pairs_closed_form(cfg1_stage):
+    st = cfg1_stage
+    pc, pi = F.count_pairs(st.group_begin, st.out_ptr, st.out_idx, 128, 4096)
+    sizes = np.diff(st.group_begin.astype(np.int64))[1:]
+    exp_c = sum(int(sizes[c - 1]) * int(sum(sizes[x - 1] for x in st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]]))
+                for c in range(1, st.num_groups + 1))
+    exp_i = int(sum(n * (n - 1) for n in sizes if 128 <= n <= 4096))
+    assert (pc, pi) == (exp_c, exp_i)
+
+
+def test_generator_deterministic_and_pinned():
+    g = load_golden("cfg1_ref.npz")
+    X1, lp1, li1 = D.generate(D.CONFIGS["cfg1"], nthreads=1)
+    X2, lp2, li2 = D.generate(D.CONFIGS["cfg1"], nthreads=8)
+    assert np.array_equal(X1, X2) and np.array_equal(lp1, lp2) and np.array_equal(li1, li2)
+    h = hashlib.sha256(X1.tobytes()).hexdigest()
+    assert h == str(g["x_sha256"])
+
+
+def test_generator_statistics():
+    cfg = D.scaled(D.CONFIGS["cfg2"], 20000)
+    X, lp, li = D.generate(cfg)
+    m = np.diff(lp.astype(np.int64))
+    assert m.min() == 1 and m.max() == 4
+    assert abs(m.mean() - 2.5) < 0.05
+    for i in range(0, 20000, 97):
+        row = li[lp[i]: lp[i + 1]]
+        assert (np.diff(row.astype(np.int64)) > 0).all() and row.min() >= 1 and row.max() <= 40
+    freq = np.bincount(li, minlength=41)[1:]
+    assert freq[0] > freq[9] > freq[39]  # Zipf ranks
+    # mixture: per-coordinate variance = scale^2 + sigma^2 = 1.09
+    assert abs(X.var() - 1.09) < 0.05
+    cfg3 = D.scaled(D.CONFIGS["cfg3"], 500)
+    X3 = D.synth_vectors(cfg3)
+    assert np.allclose(np.linalg.norm(X3, axis=1), 1.0, atol=1e-5)
+    cfg4 = D.scaled(D.CONFIGS["cfg4"], 3000)
+    lp4, li4 = D.synth_labels(cfg4)
+    for i in range(0, 3000, 31):
+        row = li4[lp4[i]: lp4[i + 1]].astype(np.int64)
+        parent = row[0]
+        assert 1 <= parent <= 10 and len(row) <= 4
+        p = parent - 1
+        assert all(11 + 9 * p <= c <= 19 + 9 * p for c in row[1:])
+
+
+def test_formats_roundtrip(tmp_path):
+    rng = np.random.default_rng(2)
+    X = rng.standard_normal((50, 9)).astype(np.float32)
+    D.write_bin(os.path.join(tmp_path, "b.bin"), X)
+    raw = open(os.path.join(tmp_path, "b.bin"), "rb").read()
+    assert np.frombuffer(raw[:8], np.uint32).tolist() == [50, 9]
+    assert np.array_equal(D.read_bin(os.path.join(tmp_path, "b.bin")), X)
+    _, lp, li = _labels(rng, 50, 8, 3, 1)
+    D.write_labels(os.path.join(tmp_path, "l.txt"), lp, li)
+    lp2, li2 = D.read_labels(os.path.join(tmp_path, "l.txt"), 50)
+    assert np.array_equal(lp, lp2) and np.array_equal(li, li2)
+    lp3, li3 = D.read_labels(os.path.join(tmp_path, "missing.txt"), 4)
+    assert lp3.tolist() == [0, 1, 2, 3, 4] and li3.tolist() == [1, 1, 1, 1]
+
+
+def test_stage_mid_groups_router(cfg1_stage):
+    st = cfg1_stage
+    sizes = np.diff(st.group_begin.astype(np.int64))[1:]
+    mids = st.mid_groups()
+    assert all(128 <= sizes[g - 1] <= 4096 for g in mids)
+    assert len(mids) == int(((sizes >= 128) & (sizes <= 4096)).sum())

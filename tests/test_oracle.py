@@ -1,0 +1,331 @@
+"""Pins the CPU oracle (oracle/ung_oracle.c) before it is trusted as the checker.
+
+Each restated function is checked against (a) the reference's own compiled code
+(oracle/_ref, when built), (b) golden fixtures written by that compiled code
+(tests/golden/), and (c) what the mathematics fixes: float64 brute force,
+closed forms and invariants, chosen so that a dropped term, a wrong index or a
+transposed operand fails.
+"""
+import hashlib
+import itertools
+
+import numpy as np
+import pytest
+
+from conftest import load_golden
+
+U = 2.0 ** -24
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+# ---------------------------------------------------------------- distance
+@pytest.mark.parametrize("dim", [1, 2, 3, 4, 5, 7, 8, 9, 11, 12, 15, 16, 17, 31, 32, 33, 100, 128, 129, 384, 768])
+def test_l2_bitexact_vs_reference_build(oracle, ref_oracle, dim):
+    rng = np.random.default_rng(dim)
+    for t in range(200):
+        a = (rng.standard_normal(dim) * rng.uniform(1e-3, 1e3)).astype(np.float32)
+        b = (rng.standard_normal(dim) * rng.uniform(1e-3, 1e3)).astype(np.float32)
+        x, y = np.float32(oracle.l2(a, b)), np.float32(ref_oracle.l2(a, b))
+        assert x.view(np.uint32) == y.view(np.uint32), (dim, t, x, y)
+
+
+@pytest.mark.parametrize("dim", [3, 8, 13, 128, 768])
+def test_l2_error_bound_vs_float64(oracle, dim):
+    rng = np.random.default_rng(100 + dim)
+    for _ in range(300):
+        a = rng.standard_normal(dim).astype(np.float32)
+        b = rng.standard_normal(dim).astype(np.float32)
+        exact = oracle.l2_f64(a, b)
+        got = oracle.l2(a, b)
+        assert abs(got - exact) <= (dim / 8 + 6) * U * exact * 1.01 + 1e-30
+
+
+def test_l2_closed_forms(oracle):
+    e = np.eye(16, dtype=np.float32)
+    assert oracle.l2(e[0], e[0]) == 0.0
+    assert oracle.l2(e[0], e[5]) == 2.0
+    a = np.array([3.0], np.float32)
+    b = np.array([-1.5], np.float32)
+    assert oracle.l2(a, b) == np.float32(20.25)
+    # summation order: with 9 elements the 9th lands in the masked tail of lane 0
+    a = np.zeros(9, np.float32)
+    a[0], a[8] = 1.0, 2.0 ** -12
+    # lane 0 accumulates 1, fold keeps s0 = 1, tail adds 2^-24 by fma -> 1 + 2^-24 rounds to 1
+    assert oracle.l2(a, np.zeros(9, np.float32)) == 1.0
+    # but when the tiny terms sit in one lane of two blocks they are summed first
+    a = np.zeros(17, np.float32)
+    a[1], a[9], a[0] = 2.0 ** -12, 2.0 ** -12, 1.0
+    # lane1: 2^-24 + 2^-24 = 2^-23 ; fold s1 = 2^-23 ; (s0 + s1) = 1 + 2^-23 exactly
+    assert oracle.l2(a, np.zeros(17, np.float32)) == np.float32(1.0 + 2.0 ** -23)
+
+
+# ---------------------------------------------------------------- queue
+def test_queue_matches_reference_build(oracle, ref_oracle):
+    rng = np.random.default_rng(3)
+    for t in range(300):
+        cap = int(rng.integers(1, 12))
+        n = int(rng.integers(0, 60))
+        ids = rng.integers(0, 40, n).astype(np.uint32)  # repeats: dedupe path of insert
+        ds = rng.integers(0, 6, n).astype(np.float32)    # ties
+        a = oracle.queue_stream(ids, ds, cap)
+        b = ref_oracle.queue_stream(ids, ds, cap)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), t
+
+
+def test_queue_equals_sorted_topk_for_unique_ids(oracle):
+    rng = np.random.default_rng(4)
+    for _ in range(200):
+        n = int(rng.integers(1, 80))
+        cap = int(rng.integers(1, 10))
+        ids = rng.permutation(1000)[:n].astype(np.uint32)
+        ds = rng.integers(0, 8, n).astype(np.float32)
+        got_i, got_d = oracle.queue_stream(ids, ds, cap)
+        order = sorted(zip(ds.tolist(), ids.tolist()))[:cap]
+        assert got_i.tolist() == [i for _, i in order]
+        assert got_d.tolist() == [d for d, _ in order]
+
+
+# ---------------------------------------------------------------- groups / LNG
+def _random_labels(rng, n, vocab, mmax, allow_empty=True):
+    rows = []
+    for _ in range(n):
+        m = int(rng.integers(0 if allow_empty else 1, mmax + 1))
+        rows.append(sorted(rng.choice(np.arange(1, vocab + 1), size=m, replace=False).tolist()))
+    lp = np.zeros(n + 1, np.uint32)
+    lp[1:] = np.cumsum([len(r) for r in rows])
+    li = np.array([v for r in rows for v in r], np.uint32)
+    return rows, lp, li
+
+
+def test_divide_groups_vs_dict(oracle):
+    rng = np.random.default_rng(8)
+    rows, lp, li = _random_labels(rng, 3000, 7, 3)
+    G, pg, gb, n2o = oracle.divide_groups(lp, li)
+    first = {}
+    for i, r in enumerate(rows):
+        first.setdefault(tuple(r), len(first) + 1)
+    assert G == len(first)
+    assert [first[tuple(r)] for r in rows] == pg.tolist()
+    expect = [i for g in range(1, G + 1) for i, r in enumerate(rows) if first[tuple(r)] == g]
+    assert n2o.tolist() == expect
+    sizes = np.bincount(pg, minlength=G + 1)[1:]
+    assert np.array_equal(np.diff(gb.astype(np.int64))[1:], sizes)
+
+
+def _minsup_python(sets):
+    G = len(sets)
+    out = []
+    for c in range(G):
+        sup = [x for x in range(G) if x != c and set(sets[c]) < set(sets[x])]
+        mins = [x for x in sup if not any(set(sets[y]) < set(sets[x]) for y in sup if y != x)]
+        out.append(sorted(x + 1 for x in mins))
+    return out
+
+
+def test_min_supersets_vs_definition(oracle):
+    rng = np.random.default_rng(9)
+    for trial in range(5):
+        universe = [tuple(sorted(s)) for m in range(0, 4) for s in itertools.combinations(range(1, 7), m)]
+        pick = rng.choice(len(universe), size=int(rng.integers(5, 40)), replace=False)
+        sets = [list(universe[i]) for i in pick]
+        sp = np.zeros(len(sets) + 2, np.uint32)
+        sp[2:] = np.cumsum([len(s) for s in sets])
+        si = np.array([v for s in sets for v in s], np.uint32)
+        op, oi = oracle.min_supersets(sp, si)
+        got = [oi[op[c]: op[c + 1]].tolist() for c in range(1, len(sets) + 1)]
+        assert got == _minsup_python(sets), trial
+
+
+# ---------------------------------------------------------------- cross edges
+@pytest.mark.parametrize("fixture", ["cfg1_ref.npz", "cfg3_6k_ref.npz"])
+def test_cross_exact_vs_golden(oracle, fixture):
+    import filtervectorcode_refactor_amd as F
+    from filtervectorcode_refactor_amd import datasets as D
+    g = load_golden(fixture)
+    cfg = D.CONFIGS["cfg1"] if fixture.startswith("cfg1") else D.scaled(D.CONFIGS["cfg3"], 6000)
+    X, lp, li = D.generate(cfg)
+    assert sha(X) == str(g["x_sha256"]) and sha(lp, li) == str(g["labels_sha256"]), "generator drift"
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    assert np.array_equal(st.out_idx, g["out_idx"]) and np.array_equal(st.group_begin, g["group_begin"])
+    ids, dists, size = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    assert np.array_equal(ids, g["cross_ids"])
+    assert np.array_equal(dists.view(np.uint32), g["cross_dists"].view(np.uint32))
+    assert np.array_equal(size, g["cross_size"])
+    assert sha(ids, dists, size) == str(g["cross_sha256"])
+
+
+def test_cross_exact_vs_reference_build(oracle, ref_oracle, cfg1_stage):
+    st = cfg1_stage
+    a = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 7)
+    b = ref_oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 7)
+    for x, y in zip(a, b):
+        assert np.array_equal(np.asarray(x).view(np.uint32) if x.dtype == np.float32 else x,
+                              np.asarray(y).view(np.uint32) if y.dtype == np.float32 else y)
+
+
+def test_cross_exact_vs_float64_bruteforce(oracle, cfg1_stage):
+    """Top-k ids equal a float64 brute force except inside the 1e-5 tie band."""
+    st = cfg1_stage
+    k = 6
+    ids, dists, size = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, k)
+    rng = np.random.default_rng(1)
+    X64 = st.base.astype(np.float64)
+    gpt = st.new_vec_id_to_group_id
+    checked = 0
+    for q in rng.choice(st.base.shape[0], 400, replace=False):
+        c = gpt[q]
+        xs = st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]]
+        if len(xs) == 0:
+            assert size[q] == 0 and (ids[q] == 0xFFFFFFFF).all()
+            continue
+        cand = np.concatenate([np.arange(st.group_begin[x], st.group_begin[x + 1]) for x in xs])
+        d64 = ((X64[cand] - X64[q]) ** 2).sum(1)
+        order = np.lexsort((cand, d64))
+        m = min(k, len(cand))
+        assert size[q] == m
+        exp = cand[order[:m]]
+        got = ids[q, :m]
+        if not np.array_equal(exp, got):
+            kth = d64[order[m - 1]]
+            diff = set(exp.tolist()) ^ set(got.tolist())
+            for v in diff:  # every disagreement must be a near tie with the boundary
+                dv = d64[np.nonzero(cand == v)[0][0]]
+                assert abs(dv - kth) <= 1e-5 * kth
+        checked += 1
+    assert checked > 100
+
+
+def test_cross_invariants(oracle, cfg1_stage):
+    st = cfg1_stage
+    ids, dists, size = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    gpt = st.new_vec_id_to_group_id
+    for q in range(0, st.base.shape[0], 7):
+        m = size[q]
+        row_i, row_d = ids[q, :m].astype(np.int64), dists[q, :m]
+        assert all((row_d[j], row_i[j]) < (row_d[j + 1], row_i[j + 1]) for j in range(m - 1))
+        c = gpt[q]
+        allowed = set(st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]].tolist())
+        assert all(int(gpt[v]) in allowed for v in row_i)
+        U_c = sum(int(st.group_begin[x + 1] - st.group_begin[x]) for x in allowed)
+        assert m == min(6, U_c)
+        assert (ids[q, m:] == 0xFFFFFFFF).all() and np.isinf(dists[q, m:]).all()
+
+
+def test_tiny_cases_vs_golden(oracle):
+    import filtervectorcode_refactor_amd as F
+    g = load_golden("tiny_cases.npz")
+    ip, ii = F.in_neighbors(g["out_ptr"], g["out_idx"])
+    for dim in (3, 7, 12):
+        for k in (1, 2, 6):
+            X = g[f"d{dim}_k{k}_X"]
+            ids, dists, size = oracle.cross_exact(X, g["group_begin"], ip, ii, k)
+            assert np.array_equal(ids, g[f"d{dim}_k{k}_ids"])
+            assert np.array_equal(dists, g[f"d{dim}_k{k}_dists"])
+            assert np.array_equal(size, g[f"d{dim}_k{k}_size"])
+        oi, od = oracle.intra_exact(g[f"d{dim}_k1_X"], 0, 6, 4)
+        assert np.array_equal(oi, g[f"d{dim}_intra_ids"]) and np.array_equal(od, g[f"d{dim}_intra_dists"])
+
+
+# ---------------------------------------------------------------- intra kNN
+@pytest.mark.parametrize("fixture", ["cfg1_ref.npz", "cfg3_6k_ref.npz"])
+def test_intra_exact_vs_golden(oracle, fixture):
+    import filtervectorcode_refactor_amd as F
+    from filtervectorcode_refactor_amd import datasets as D
+    g = load_golden(fixture)
+    cfg = D.CONFIGS["cfg1"] if fixture.startswith("cfg1") else D.scaled(D.CONFIGS["cfg3"], 6000)
+    X, lp, li = D.generate(cfg)
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    K = int(g["intra_k"])
+    all_i, all_d = [], []
+    for gid in g["intra_groups"]:
+        b, e = int(st.group_begin[gid]), int(st.group_begin[gid + 1])
+        oi, od = oracle.intra_exact(st.base, b, e - b, K)
+        all_i.append(oi)
+        all_d.append(od)
+    all_i, all_d = np.concatenate(all_i), np.concatenate(all_d)
+    assert sha(all_i, all_d) == str(g["intra_sha256"])
+    rows = g["intra_rows"]
+    assert np.array_equal(all_i[rows].astype(np.uint16), g["intra_ids"])
+    assert np.array_equal(all_d[rows], g["intra_dists"])
+
+
+def test_intra_exact_vs_float64(oracle):
+    rng = np.random.default_rng(12)
+    X = rng.standard_normal((300, 24)).astype(np.float32)
+    n, K = 250, 10
+    ids, dists = oracle.intra_exact(X, 20, n, K)
+    G = X[20:20 + n].astype(np.float64)
+    for i in range(0, n, 5):
+        d64 = ((G - G[i]) ** 2).sum(1)
+        d64[i] = np.inf
+        order = np.lexsort((np.arange(n), d64))[:K]
+        if not np.array_equal(order, ids[i]):
+            kth = d64[order[-1]]
+            for v in set(order.tolist()) ^ set(ids[i].tolist()):
+                assert abs(d64[v] - kth) <= 1e-5 * kth
+
+
+def test_intra_small_groups(oracle):
+    X = np.arange(12, dtype=np.float32).reshape(6, 2)
+    ids, dists = oracle.intra_exact(X, 0, 1, 4)
+    assert (ids == 0xFFFFFFFF).all()
+    ids, dists = oracle.intra_exact(X, 2, 2, 4)
+    assert ids[0].tolist()[:1] == [1] and ids[1].tolist()[:1] == [0]
+    assert (ids[:, 1:] == 0xFFFFFFFF).all()
+
+
+# ---------------------------------------------------------------- anchor packing
+def test_pack_anchor_hand_worked(oracle):
+    # n=10, local_src=3, final_degree=4, head_keep=2, anchors: remaining=2 -> hops
+    # (t+1)*10//3 = 3, 6 -> candidates 6, 9 ; cand_degree=5
+    top = np.array([4, 2, 7, 8, 1], np.uint32)
+    row = oracle.pack_anchor_row(top, 5, 10, 3, 4, 2)
+    assert row.tolist() == [4, 4, 2, 6, 9]
+    # anchor collides with the head (hop to 4 which is taken) -> linear probe to 5
+    top = np.array([4, 5, 7, 8, 1], np.uint32)
+    row = oracle.pack_anchor_row(top, 5, 10, 1, 4, 2)  # hops 3 -> 4 (dup), 5 (dup) -> 6 ; 6 -> 7
+    assert row.tolist() == [4, 4, 5, 6, 7]
+    # no anchors: strided tail then dedup tail; stride = ceil(tail/remaining)
+    top = np.array([9, 8, 7, 6, 5, 4, 3], np.uint32)
+    row = oracle.pack_anchor_row(top, 7, 12, 0, 4, 1, anchor_tail=0)
+    # tail_count=6, remaining=3, step=2 -> positions 1,3,5 -> 8,6,4
+    assert row.tolist() == [4, 9, 8, 6, 4]
+    # out_degree smaller than final_degree: padding with local_src
+    top = np.array([1, 2], np.uint32)
+    row = oracle.pack_anchor_row(top, 2, 3, 0, 4, 2)
+    assert row.tolist() == [2, 1, 2, 0, 0]
+    # backward anchors (bidir): t odd goes backward
+    top = np.array([1, 2, 3, 4, 5, 6], np.uint32)
+    row = oracle.pack_anchor_row(top, 6, 12, 0, 4, 2, anchor_tail=1, bidir_anchor=1)
+    # remaining 2: hops 4, 8 ; t=0 fwd -> 4 (dup? head is 1,2 -> no) ; t=1 bwd -> (0+12-8)%12 = 4 dup -> 3
+    assert row.tolist() == [4, 1, 2, 4, 3]
+
+
+def test_pack_anchor_invariants(oracle):
+    rng = np.random.default_rng(13)
+    for _ in range(300):
+        n = int(rng.integers(2, 200))
+        src = int(rng.integers(0, n))
+        others = np.array([v for v in rng.permutation(n) if v != src], np.uint32)
+        cd = min(63, n - 1)
+        fd = int(rng.integers(1, 40))
+        hk = int(rng.integers(1, fd + 1))
+        tail = int(rng.integers(0, 2))
+        row = oracle.pack_anchor_row(others[:cd], cd, n, src, fd, hk, anchor_tail=tail,
+                                     bidir_anchor=int(rng.integers(0, 2)))
+        od = min(fd, cd)
+        assert row[0] == od
+        body = row[1: 1 + od].tolist()
+        assert src not in body
+        assert body[: min(hk, od)] == others[: min(hk, od)].tolist()
+        if tail == 1:
+            assert len(set(body)) == len(body)
+        assert (row[1 + od:] == src).all()
