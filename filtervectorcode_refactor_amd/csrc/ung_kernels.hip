@@ -24,6 +24,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -40,8 +41,10 @@ constexpr int BC = 128;          // candidates per tile (rows of the MFMA tiles)
 constexpr int KC = 32;           // k-chunk staged in LDS
 constexpr int LDSW = KC + 4;     // padded LDS row stride (floats)
 constexpr int NTHREADS = 256;    // 4 waves: 2 (candidate halves) x 2 (query halves)
-constexpr uint32_t SPLIT_V = 16384; // max candidates per work item (load balance)
-constexpr uint32_t MERGE_Q = 256;   // rows per merge block
+constexpr uint32_t SPLIT_V = 16384; // candidates per work item (raised so a job has <= 64 splits)
+constexpr uint32_t MAX_SPLITS = 64; // one wave lane per split in the merge
+constexpr uint32_t MERGE_ROWS = 4;  // result rows (one wave each) per merge block
+constexpr uint32_t MERGE_Q = 256;   // rows per packing block
 constexpr uint32_t NONE = 0xFFFFFFFFu;
 
 struct Job {
@@ -52,6 +55,7 @@ struct Job {
     uint32_t out_row;              // result row of query 0
     uint32_t id_base;              // subtracted from result ids (group begin for local ids)
     uint32_t flags;                // bit 0: exclude the query itself
+    uint32_t split_v;              // candidates per split
 };
 
 struct Item {
@@ -79,6 +83,9 @@ struct SelectParams {
     double eps_coef;  // 2*(d+4)*2^-24 : expansion-form error factor on (|q|+R)^2
     double shrink;    // (d/8+8)*2^-24 : relative error of the reference summation
     double rmax;      // max candidate norm (slightly inflated)
+    uint32_t n_items; // items of this launch
+    uint32_t xcd_chunk; // XCD chunking of the item order (0 = identity)
+    uint32_t lp;      // entries per partial row (approximate top-Lp)
 };
 
 // ---------------------------------------------------------------------------
@@ -197,44 +204,137 @@ __device__ __forceinline__ void list_insert(float (&ld)[LT], uint32_t (&li)[LT],
 //   |a - D| <= eps_coef * (|q| + R)^2   (norm cache, MFMA dot, epilogue roundings)
 //   e >= D * (1 - shrink)               (reference summation)
 // Rounded toward -inf when narrowed to fp32.
-__device__ __forceinline__ float lower_bound_exact(float A, float qn, const SelectParams &P)
+__device__ __forceinline__ float lower_bound_exact(float A, float qn, double eps_coef, double shrink, double rmax)
 {
     if (!(A < INFINITY))
         return INFINITY;
     const double qnorm = sqrt((double)fmaxf(qn, 0.0f) * (1.0 + 1e-6));
-    const double r = qnorm + P.rmax;
-    const double ea = P.eps_coef * r * r;
+    const double r = qnorm + rmax;
+    const double ea = eps_coef * r * r;
     double b = ((double)A - ea);
-    b = b > 0.0 ? b * (1.0 - P.shrink) : b * (1.0 + P.shrink);
+    b = b > 0.0 ? b * (1.0 - shrink) : b * (1.0 + shrink);
     b -= 1e-30;
     return __double2float_rd(b);
+}
+
+// (dist, id) argmin across the wave; every lane ends with the minimum.
+__device__ __forceinline__ void wave_argmin(float &d, uint32_t &i)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float od = __shfl_xor(d, off);
+        const uint32_t oi = __shfl_xor(i, off);
+        if (cand_less(od, oi, d, i)) {
+            d = od;
+            i = oi;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
 // select kernel
 // ---------------------------------------------------------------------------
-struct SelectSmem {
+struct alignas(16) SelectSmem {
     union {
         struct {
-            float qs[2][BQ][LDSW];
-            float xs[2][BC][LDSW];
+            // float4-typed so every panel access is a 16-byte ds_read/ds_write_b128
+            float4 qs[2][BQ][LDSW / 4];
+            float4 xs[2][BC][LDSW / 4];
         } p;
         struct {
             float ed[64][129];   // entry distances (approx, then exact); stride padded
             uint32_t ei[64][129];
-            float alist[64][4];  // LT-th approx of each queue (+inf when not full)
+            float alist[64][4];  // per queue: bound on every candidate it did not keep
+            float drop[64];      // smallest queued value not written to the partial row
         } r;
     } u;
-    uint32_t rowid[BC];
-    float xnr[BC];
+    uint32_t rowid[3][BC]; // candidate ids of tiles t%3 (ring: built one tile ahead)
+    float4 xnr[3][BC / 4]; // their half squared norms (+inf for padding rows), 4 rows per float4
     float qn[BQ];
+    float tau[2][2][BQ];   // [tile parity][candidate wave][query]: a wave's queue threshold
 };
 
-template <int LT, bool VEC4>
-__global__ __launch_bounds__(NTHREADS, (LT <= 16 ? 2 : 1)) void ung_select_kernel(SelectParams P)
+// Logical work item of a block.  Blocks are dispatched round-robin over the 8 XCDs
+// (blockIdx % 8).  With chunk c > 0 the logical items are cut into chunks of c
+// consecutive items -- query blocks of one job that stream the same candidate
+// rows -- and chunk i runs on XCD i % 8, so a chunk shares one L2 while the chunks
+// stay interleaved across XCDs for balance.  The grid is padded to a multiple of
+// 8c; returns NONE for padding blocks.  c = 0: identity.
+__device__ __forceinline__ uint32_t xcd_logical_block(uint32_t b, uint32_t n, uint32_t c)
+{
+    if (c == 0)
+        return b;
+    const uint32_t x = b & 7u, j = b >> 3;
+    const uint32_t L = ((j / c) * 8u + x) * c + (j % c);
+    return L < n ? L : NONE;
+}
+
+// Tile row of a lane's j-th value of one query column (j = 16*mb + i of acc[mb][nb][i]).
+__device__ __forceinline__ int row_of(int wm, int h, int j)
+{
+    const int mb = j >> 4, i = j & 15;
+    return wm * 64 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+}
+
+// acc[j>>4][nb][j&15] for a per-lane index j, as a 5-level select tree over registers.
+__device__ __forceinline__ float select32(const floatx16 (&acc)[2][2], int nb, uint32_t j)
+{
+    float l16[16];
+    const bool b4 = (j & 16u) != 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        l16[i] = b4 ? acc[1][nb][i] : acc[0][nb][i];
+    float l8[8];
+    const bool b0 = (j & 1u) != 0;
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+        l8[a] = b0 ? l16[2 * a + 1] : l16[2 * a];
+    float l4[4];
+    const bool b1 = (j & 2u) != 0;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+        l4[a] = b1 ? l8[2 * a + 1] : l8[2 * a];
+    const bool b2 = (j & 4u) != 0, b3 = (j & 8u) != 0;
+    const float l2a = b2 ? l4[1] : l4[0];
+    const float l2b = b2 ? l4[3] : l4[2];
+    return b3 ? l2b : l2a;
+}
+
+// Pre-filter bound in s-space: s = |x|^2/2 - <x,q> and a = fl(2s + |q|^2).  Returns c
+// with  s >= c  =>  a >= thr  (the margin covers the rounding of 2s + |q|^2), so a
+// candidate failing s < c can never pass the exact test a < thr.
+__device__ __forceinline__ float s_bound(float thr, float qn)
+{
+    if (!(thr < INFINITY))
+        return INFINITY;
+    return 0.5f * (thr - qn) + 0x1p-20f * (fabsf(thr) + fabsf(qn));
+}
+
+// Fills the row-id ring slot for the candidate tile starting at virtual index v0.
+__device__ __forceinline__ void build_rowids(SelectSmem &sm, int slot, const SelectParams &P, const Job &jb,
+                                             uint32_t v0, uint32_t v_end, int tid)
+{
+    if (tid < BC) {
+        const uint32_t v = v0 + (uint32_t)tid;
+        uint32_t g = NONE;
+        float nx = INFINITY;
+        if (v < v_end) {
+            g = cand_id(P.seg_start, P.seg_vend, jb.seg_begin, jb.seg_count, v);
+            nx = P.xn[g];
+        }
+        sm.rowid[slot][tid] = g;
+        reinterpret_cast<float *>(sm.xnr[slot])[tid] = 0.5f * nx; // |x|^2/2 (exact scaling)
+    }
+}
+
+template <int LT, bool VEC4, bool EXCL>
+__global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
 {
     __shared__ SelectSmem sm;
-    const Item it = P.items[blockIdx.x];
+    const uint32_t logical = xcd_logical_block(blockIdx.x, P.n_items, P.xcd_chunk);
+    if (logical == NONE)
+        return;
+    const Item it = P.items[logical];
     const Job jb = P.jobs[it.job];
     const uint32_t d = P.d;
     const int tid = threadIdx.x;
@@ -243,14 +343,15 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 16 ? 2 : 1)) void ung_select_kerne
     const int r = lane & 31, h = lane >> 5;
     const uint32_t q0 = jb.q_begin + it.q_off;
     const uint32_t qcnt = it.q_cnt;
-    const bool excl = (jb.flags & 1u) != 0;
     const float *__restrict__ X = P.X;
 
     if (tid < BQ)
         sm.qn[tid] = (uint32_t)tid < qcnt ? P.xn[q0 + tid] : 0.0f;
+    build_rowids(sm, 0, P, jb, it.v_begin, it.v_end, tid);
 
     float ld[2][LT];
     uint32_t li[2][LT];
+    float tfin[2] = {INFINITY, INFINITY}; // lowest threshold a queue has applied so far
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -258,6 +359,9 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 16 ? 2 : 1)) void ung_select_kerne
             ld[nb][j] = INFINITY;
             li[nb][j] = NONE;
         }
+    // thresholds may be shared between a query's queues only when one queue's LT
+    // entries already cover the k results
+    const bool share = P.k <= (uint32_t)LT;
 
     // loader mapping: rows lr = (tid>>3) + 32m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
@@ -280,125 +384,206 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 16 ? 2 : 1)) void ung_select_kerne
         qnv[nb] = sm.qn[ql];
     }
 
-    for (uint32_t v0 = it.v_begin; v0 < it.v_end; v0 += BC) {
-        __syncthreads(); // previous epilogue done with rowid / panels
-        if (tid < BC) {
-            const uint32_t v = v0 + (uint32_t)tid;
-            uint32_t g = NONE;
-            float nx = 0.0f;
-            if (v < it.v_end) {
-                g = cand_id(P.seg_start, P.seg_vend, jb.seg_begin, jb.seg_count, v);
-                nx = P.xn[g];
-            }
-            sm.rowid[tid] = g;
-            sm.xnr[tid] = nx;
-        }
-        __syncthreads();
-        const float *xrow[4];
+    // One flat software pipeline over (candidate tile, k-chunk) steps: the panels are
+    // double-buffered in LDS and each step prefetches the next step's chunk (also
+    // across tile boundaries) into registers; the row-id table of tile t+1 is built
+    // in ring slot (t+1)%3 while tile t computes.
+    const uint32_t ntiles = (it.v_end - it.v_begin + BC - 1) / BC;
+    const uint32_t nk = (d + KC - 1) / KC;
+    const uint32_t total = ntiles * nk;
+
+    const float *xrow[4];
+    auto set_xrows = [&](int slot) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            uint32_t g = sm.rowid[lr0 + 32 * m];
-            g = (g == NONE) ? sm.rowid[0] : g;
+            uint32_t g = sm.rowid[slot][lr0 + 32 * m];
+            g = (g == NONE) ? sm.rowid[slot][0] : g;
             xrow[m] = X + (size_t)g * d;
         }
-
-        floatx16 acc[2][2];
+    };
+    float4 rq[4], rx[4];
+    auto load_chunk = [&](uint32_t kc) {
+        const uint32_t col = kc + (uint32_t)c4;
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    acc[a][b][i] = 0.0f;
-
-        float4 rq[4], rx[4];
-        auto load_chunk = [&](uint32_t kc) {
-            const uint32_t col = kc + (uint32_t)c4;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                if (VEC4) {
-                    if (col < d) {
-                        rq[m] = *reinterpret_cast<const float4 *>(qrow[m] + col);
-                        rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + col);
-                    } else {
-                        rq[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-                        rx[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    }
+        for (int m = 0; m < 4; ++m) {
+            if (VEC4) {
+                if (col < d) {
+                    rq[m] = *reinterpret_cast<const float4 *>(qrow[m] + col);
+                    rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + col);
                 } else {
-                    float tq[4], tx[4];
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const bool ok = col + t < d;
-                        tq[t] = ok ? qrow[m][col + t] : 0.0f;
-                        tx[t] = ok ? xrow[m][col + t] : 0.0f;
-                    }
-                    rq[m] = make_float4(tq[0], tq[1], tq[2], tq[3]);
-                    rx[m] = make_float4(tx[0], tx[1], tx[2], tx[3]);
+                    rq[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    rx[m] = make_float4(0.f, 0.f, 0.f, 0.f);
                 }
-            }
-        };
-
-        load_chunk(0);
-        int buf = 0;
-        for (uint32_t kc = 0; kc < d; kc += KC, buf ^= 1) {
+            } else {
+                float tq[4], tx[4];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                *reinterpret_cast<float4 *>(&sm.u.p.qs[buf][lr0 + 32 * m][c4]) = rq[m];
-                *reinterpret_cast<float4 *>(&sm.u.p.xs[buf][lr0 + 32 * m][c4]) = rx[m];
-            }
-            __syncthreads();
-            if (kc + KC < d)
-                load_chunk(kc + KC);
-            // 16 MFMA k-steps: step t covers dims kc+t (lanes h=0) and kc+16+t (h=1)
-#pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4) {
-                const int kk = h * 16 + s4 * 4;
-                const float4 a0 = *reinterpret_cast<const float4 *>(&sm.u.p.xs[buf][wm * 64 + r][kk]);
-                const float4 a1 = *reinterpret_cast<const float4 *>(&sm.u.p.xs[buf][wm * 64 + 32 + r][kk]);
-                const float4 b0 = *reinterpret_cast<const float4 *>(&sm.u.p.qs[buf][wn * 64 + r][kk]);
-                const float4 b1 = *reinterpret_cast<const float4 *>(&sm.u.p.qs[buf][wn * 64 + 32 + r][kk]);
-                const float av0[4] = {a0.x, a0.y, a0.z, a0.w};
-                const float av1[4] = {a1.x, a1.y, a1.z, a1.w};
-                const float bv0[4] = {b0.x, b0.y, b0.z, b0.w};
-                const float bv1[4] = {b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[c], bv0[c], acc[0][0], 0, 0, 0);
-                    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[c], bv1[c], acc[0][1], 0, 0, 0);
-                    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[c], bv0[c], acc[1][0], 0, 0, 0);
-                    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[c], bv1[c], acc[1][1], 0, 0, 0);
+                for (int t = 0; t < 4; ++t) {
+                    const bool ok = col + t < d;
+                    tq[t] = ok ? qrow[m][col + t] : 0.0f;
+                    tx[t] = ok ? xrow[m][col + t] : 0.0f;
                 }
+                rq[m] = make_float4(tq[0], tq[1], tq[2], tq[3]);
+                rx[m] = make_float4(tx[0], tx[1], tx[2], tx[3]);
             }
         }
+    };
 
-        // epilogue: acc[mb][nb][i] = <x_row, q_col>, row = wm*64+mb*32+8*(i/4)+4*h+(i%4),
-        // col = wn*64+nb*32+r
+    floatx16 acc[2][2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                acc[a][b][i] = 0.0f;
+
+    __syncthreads(); // ring slot 0 and qn visible
+    set_xrows(0);
+    load_chunk(0);
+
+    uint32_t tile = 0, kc = 0;
+    int slot = 0;
+    for (uint32_t s = 0; s < total; ++s) {
+        const int buf = (int)(s & 1u);
+        const int next_slot = slot == 2 ? 0 : slot + 1;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            sm.u.p.qs[buf][lr0 + 32 * m][c4 >> 2] = rq[m];
+            sm.u.p.xs[buf][lr0 + 32 * m][c4 >> 2] = rx[m];
+        }
+        if (nk == 1 && tile + 1 < ntiles)
+            build_rowids(sm, next_slot, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
+        __syncthreads();
+        if (s + 1 < total) {
+            if (kc + 1 == nk) {
+                set_xrows(next_slot);
+                load_chunk(0);
+            } else {
+                load_chunk((kc + 1) * KC);
+            }
+        }
+        // 16 MFMA k-steps: step t covers dims kc*KC+t (lanes h=0) and kc*KC+16+t (h=1)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int kk = h * 4 + s4; // float4 column: dims 16h + 4*s4 .. +3
+            const float4 a0 = sm.u.p.xs[buf][wm * 64 + r][kk];
+            const float4 a1 = sm.u.p.xs[buf][wm * 64 + 32 + r][kk];
+            const float4 b0 = sm.u.p.qs[buf][wn * 64 + r][kk];
+            const float4 b1 = sm.u.p.qs[buf][wn * 64 + 32 + r][kk];
+            const float av0[4] = {a0.x, a0.y, a0.z, a0.w};
+            const float av1[4] = {a1.x, a1.y, a1.z, a1.w};
+            const float bv0[4] = {b0.x, b0.y, b0.z, b0.w};
+            const float bv1[4] = {b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[c], bv0[c], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[c], bv1[c], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[c], bv0[c], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[c], bv1[c], acc[1][1], 0, 0, 0);
+            }
+        }
+        // next tile's row ids: issued after this step's MFMAs, visible after the next
+        // step's barrier, consumed by the prefetch of the tile's first chunk
+        if (nk > 1 && kc == 0 && tile + 1 < ntiles)
+            build_rowids(sm, next_slot, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
+
+        if (kc + 1 == nk) {
+            // epilogue: acc[mb][nb][i] = <x_row, q_col>, row = wm*64+mb*32+8*(i/4)+4*h+(i%4),
+            // col = wn*64+nb*32+r.  s = |x|^2/2 - <x,q> and the expansion-form distance is
+            // a = fl(2s + |q|^2) (padding rows: |x|^2 = +inf).
+            //
+            // The four queues of a query (lane halves h, candidate waves wm) share a
+            // threshold: a candidate is queued only if a < min(own LT-th, partner lane's,
+            // other wave's of the previous tile).  Any candidate with a >= that value can
+            // not be among the query's LT best (one queue already holds LT better ones),
+            // and thresholds only decrease, so a stale value is safe.
+            float tsh[2], cth[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const int col = wn * 64 + nb * 32 + r;
+                const float own = ld[nb][LT - 1];
+                const float partner = __shfl_xor(own, 32);
+                float t = fminf(own, tfin[nb]);
+                if (share) {
+                    t = fminf(t, partner);
+                    if (tile > 0)
+                        t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col]);
+                }
+                tsh[nb] = t;
+                cth[nb] = s_bound(t, qnv[nb]);
+            }
+            // branch-free pass: s in place of acc, and per list a lane mask whose bit
+            // (31 - j) marks element j under the pre-filter bound
+            uint32_t pend[2] = {0u, 0u};
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) {
+                float4 xq[4];
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4)
+                    xq[g4] = sm.xnr[slot][(wm * 64 + mb * 32 + 8 * g4 + 4 * h) >> 2];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int row = wm * 64 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                    const uint32_t g = sm.rowid[row];
-                    float dd = __builtin_fmaf(-2.0f, acc[mb][nb][i], qnv[nb] + sm.xnr[row]);
-                    const bool valid = (g != NONE) && !(excl && g == qid[nb]);
-                    dd = valid ? dd : INFINITY;
-                    const bool p = dd < ld[nb][LT - 1];
-                    if (__ballot(p)) {
-                        if (p)
-                            list_insert<LT>(ld[nb], li[nb], dd, g);
+                    const float4 x4 = xq[i >> 2];
+                    const float hxv = (i & 3) == 0 ? x4.x : (i & 3) == 1 ? x4.y : (i & 3) == 2 ? x4.z : x4.w;
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        float sv = hxv - acc[mb][nb][i];
+                        if (EXCL) {
+                            const int row = wm * 64 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                            sv = sm.rowid[slot][row] == qid[nb] ? INFINITY : sv;
+                        }
+                        acc[mb][nb][i] = sv;
+                        pend[nb] = (pend[nb] << 1) | (sv < cth[nb] ? 1u : 0u);
                     }
                 }
             }
+            // rounds: each lane inserts at most one pending element per list per round
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                uint32_t m = pend[nb];
+                while (__ballot(m != 0u)) {
+                    if (m != 0u) {
+                        const uint32_t j = (uint32_t)__builtin_clz(m);
+                        m &= ~(0x80000000u >> j);
+                        const float dd = __builtin_fmaf(2.0f, select32(acc, nb, j), qnv[nb]);
+                        if (dd < fminf(ld[nb][LT - 1], tsh[nb])) {
+                            list_insert<LT>(ld[nb], li[nb], dd, sm.rowid[slot][row_of(wm, h, (int)j)]);
+                            tsh[nb] = fminf(tsh[nb], ld[nb][LT - 1]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        acc[mb][nb][i] = 0.0f;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                // publish this wave's threshold of the query for the other wave
+                const float t = fminf(tsh[nb], ld[nb][LT - 1]);
+                tfin[nb] = t;
+                const float pair_t = fminf(t, __shfl_xor(t, 32));
+                if (share && h == 0)
+                    sm.tau[tile & 1][wm][wn * 64 + nb * 32 + r] = pair_t;
+            }
+            ++tile;
+            kc = 0;
+            slot = next_slot;
+        } else {
+            ++kc;
         }
     }
 
-    // ---- exact re-score of the queued candidates, two passes of 64 queries ----
+    // ---- per query: the Lp best queued candidates by approximate distance, and a
+    // bound every other candidate of this split satisfies (two passes of 64 queries) ----
     constexpr int E = 4 * LT;
-    const int sub = tid & 7;
-    const int grp = tid >> 3; // 32 groups of 8 lanes
-    for (int pass = 0; pass < 2; ++pass) {
+    const uint32_t Lp = P.lp;
+    const int npass = qcnt > 64 ? 2 : 1;
+    for (int pass = 0; pass < npass; ++pass) {
+        const int rows_here = (int)min(64u, qcnt - (uint32_t)pass * 64u);
         __syncthreads();
         if (wn == pass) {
             const int lid = wm * 2 + h;
@@ -410,49 +595,44 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 16 ? 2 : 1)) void ung_select_kerne
                     sm.u.r.ed[jl][lid * LT + j] = ld[nb][j];
                     sm.u.r.ei[jl][lid * LT + j] = li[nb][j];
                 }
-                sm.u.r.alist[jl][lid] = ld[nb][LT - 1];
+                // every candidate this queue never kept has a >= this value
+                sm.u.r.alist[jl][lid] = fminf(ld[nb][LT - 1], tfin[nb]);
             }
         }
+        if (tid < 64)
+            sm.u.r.drop[tid] = INFINITY;
         __syncthreads();
-        for (int p = grp; p < 64 * E; p += 32) {
+        // rank of every entry under (approx, id, slot)
+        for (int p = tid; p < rows_here * E; p += NTHREADS) {
             const int jl = p / E, e = p % E;
             const uint32_t ql = (uint32_t)(pass * 64 + jl);
-            const uint32_t id = sm.u.r.ei[jl][e];
-            const bool ok = id != NONE && ql < qcnt;
-            const float *a = X + (size_t)(q0 + (ql < qcnt ? ql : 0u)) * d;
-            const float *b = X + (size_t)(ok ? id : q0) * d;
-            const float ex = l2_ref_8lane(a, b, d, sub);
-            if (sub == 0)
-                sm.u.r.ed[jl][e] = ok ? ex : INFINITY;
-        }
-        __syncthreads();
-        // rank of every entry under (exact, id, slot); the k best go to the partial row
-        for (int p = tid; p < 64 * E; p += NTHREADS) {
-            const int jl = p / E, e = p % E;
-            const uint32_t ql = (uint32_t)(pass * 64 + jl);
-            if (ql >= qcnt)
-                continue;
             const float de = sm.u.r.ed[jl][e];
             const uint32_t ie = sm.u.r.ei[jl][e];
-            int rank = 0;
+            uint32_t rank = 0;
             for (int f = 0; f < E; ++f) {
                 const float df = sm.u.r.ed[jl][f];
                 const uint32_t idf = sm.u.r.ei[jl][f];
-                rank += (df < de || (df == de && (idf < ie || (idf == ie && f < e)))) ? 1 : 0;
+                rank += (df < de || (df == de && (idf < ie || (idf == ie && f < e)))) ? 1u : 0u;
             }
-            const uint32_t prow = jb.part_base + it.split * jb.q_count + it.q_off + ql;
-            if ((uint32_t)rank < P.k) {
+            const size_t prow = (size_t)jb.part_base + (size_t)it.split * jb.q_count + it.q_off + ql;
+            if (rank < Lp) {
                 const bool real = ie != NONE && de < INFINITY;
-                P.part_ids[(size_t)prow * P.k + rank] = real ? ie : NONE;
-                P.part_dist[(size_t)prow * P.k + rank] = real ? de : INFINITY;
+                P.part_ids[prow * Lp + rank] = real ? ie : NONE;
+                P.part_dist[prow * Lp + rank] = real ? de : INFINITY;
+            } else if (rank == Lp) {
+                sm.u.r.drop[jl] = de; // smallest queued value left out of the partial row
             }
-            if (e == 0) {
-                float A = sm.u.r.alist[jl][0];
+        }
+        __syncthreads();
+        if (tid < rows_here) {
+            const int jl = tid;
+            const uint32_t ql = (uint32_t)(pass * 64 + jl);
+            float A = sm.u.r.drop[jl];
 #pragma unroll
-                for (int l = 1; l < 4; ++l)
-                    A = fminf(A, sm.u.r.alist[jl][l]);
-                P.part_bound[prow] = lower_bound_exact(A, sm.qn[ql], P);
-            }
+            for (int l = 0; l < 4; ++l)
+                A = fminf(A, sm.u.r.alist[jl][l]);
+            const size_t prow = (size_t)jb.part_base + (size_t)it.split * jb.q_count + it.q_off + ql;
+            P.part_bound[prow] = A; // approximate-distance space
         }
     }
 }
@@ -461,12 +641,17 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 16 ? 2 : 1)) void ung_select_kerne
 // merge + certification
 // ---------------------------------------------------------------------------
 struct MergeParams {
+    const float *X;
+    const float *xn;
+    uint32_t d;
     const Job *jobs;
-    const MergeItem *mitems;
+    const MergeItem *mitems; // q_cnt <= MERGE_ROWS: one wave per result row
     const uint32_t *part_ids;
     const float *part_dist;
     const float *part_bound;
+    uint32_t lp;
     uint32_t k;
+    double eps_coef, shrink, rmax;
     uint32_t *out_ids;
     float *out_dist;
     int32_t *out_size;
@@ -474,72 +659,109 @@ struct MergeParams {
     uint2 *flagged;
 };
 
-template <int KM>
-__global__ __launch_bounds__(MERGE_Q) void ung_merge_kernel(MergeParams M)
+// One wave per result row: k-way merge of the row's S partial rows (S <= 64, each
+// sorted by approximate distance) to its Lp best approximate candidates, exact
+// re-score of those in the reference's summation order, (dist, id) ranking, and the
+// certificate  T_k < lower bound of every candidate left out.
+__global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams M)
 {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const MergeItem mi = M.mitems[blockIdx.x];
-    if (threadIdx.x >= mi.q_cnt)
-        return;
+    if ((uint32_t)w >= mi.q_cnt)
+        return; // whole wave; no block barrier below
     const Job jb = M.jobs[mi.job];
-    const uint32_t ql = mi.q_off + threadIdx.x;
-    const uint32_t k = M.k;
-    float bd[KM];
-    uint32_t bi[KM];
-#pragma unroll
-    for (int j = 0; j < KM; ++j) {
-        bd[j] = INFINITY;
-        bi[j] = NONE;
+    const uint32_t ql = mi.q_off + (uint32_t)w;
+    const uint32_t q = jb.q_begin + ql;
+    const uint32_t S = jb.n_split, Lp = M.lp, k = M.k;
+
+    size_t prow = 0;
+    uint32_t pos = 0;
+    float hd = INFINITY, bnd = INFINITY;
+    uint32_t hi = NONE;
+    if ((uint32_t)lane < S) {
+        prow = (size_t)jb.part_base + (size_t)lane * jb.q_count + ql;
+        bnd = M.part_bound[prow];
+        hd = M.part_dist[prow * Lp];
+        hi = M.part_ids[prow * Lp];
     }
-    float bmin = INFINITY;
-    for (uint32_t s = 0; s < jb.n_split; ++s) {
-        const size_t prow = (size_t)jb.part_base + (size_t)s * jb.q_count + ql;
-        bmin = fminf(bmin, M.part_bound[prow]);
-        for (uint32_t j = 0; j < k; ++j) {
-            const uint32_t id = M.part_ids[prow * k + j];
-            if (id == NONE)
-                break;
-            float nd = M.part_dist[prow * k + j];
-            uint32_t ni = id;
-            // (dist,id)-ordered insertion into the running top-KM
+    float bmin = bnd;
 #pragma unroll
-            for (int t = 0; t < KM; ++t) {
-                const bool sw = cand_less(nd, ni, bd[t], bi[t]);
-                const float td = bd[t];
-                const uint32_t ti = bi[t];
-                bd[t] = sw ? nd : td;
-                bi[t] = sw ? ni : ti;
-                nd = sw ? td : nd;
-                ni = sw ? ti : ni;
+    for (int off = 32; off > 0; off >>= 1)
+        bmin = fminf(bmin, __shfl_xor(bmin, off));
+
+    // lane t < Lp receives the t-th smallest approximate candidate
+    float a_next = INFINITY;
+    uint32_t ci = NONE;
+    for (uint32_t t = 0; t <= Lp; ++t) {
+        float bd = hd;
+        uint32_t bi = hi;
+        wave_argmin(bd, bi);
+        if (bi == NONE)
+            break; // every head is exhausted (uniform)
+        if (t == Lp) {
+            a_next = bd;
+            break;
+        }
+        if ((uint32_t)lane == t)
+            ci = bi;
+        if (hi == bi) {
+            ++pos;
+            if (pos < Lp) {
+                hd = M.part_dist[prow * Lp + pos];
+                hi = M.part_ids[prow * Lp + pos];
+            } else {
+                hd = INFINITY;
+                hi = NONE;
             }
         }
     }
-    uint32_t count = 0;
+    const float B = fminf(bmin, a_next); // approximate-space bound of everything left out
+
+    // exact re-score: 8 groups of 8 lanes, candidate e = base + group
+    const int sub = lane & 7, grp = lane >> 3;
+    const float *qv = M.X + (size_t)q * M.d;
+    float ex = INFINITY;
+    for (uint32_t base = 0; base < Lp; base += 8) {
+        const uint32_t e = base + (uint32_t)grp;
+        const uint32_t id = __shfl(ci, (int)(e < 64u ? e : 63u));
+        float v = INFINITY;
+        if (e < Lp && id != NONE) // uniform inside the 8-lane group
+            v = l2_ref_8lane(qv, M.X + (size_t)id * M.d, M.d, sub);
+        const float got = __shfl(v, (int)((((uint32_t)lane - base) & 7u) * 8u));
+        if ((uint32_t)lane >= base && (uint32_t)lane < base + 8u)
+            ex = got;
+    }
+    // rank under (exact, id, lane)
+    uint32_t rank = 0;
+    for (uint32_t f = 0; f < Lp; ++f) {
+        const float df = __shfl(ex, (int)f);
+        const uint32_t idf = __shfl(ci, (int)f);
+        rank += (df < ex || (df == ex && (idf < ci || (idf == ci && f < (uint32_t)lane)))) ? 1u : 0u;
+    }
+    const bool mine = (uint32_t)lane < Lp;
+    const bool real = mine && ci != NONE;
+    float T = (mine && rank == k - 1) ? ex : INFINITY;
 #pragma unroll
-    for (int t = 0; t < KM; ++t)
-        count += ((uint32_t)t < k && bi[t] != NONE) ? 1u : 0u;
-    float T = INFINITY;
-#pragma unroll
-    for (int t = 0; t < KM; ++t)
-        if ((uint32_t)t == k - 1)
-            T = bd[t];
-    const bool certified = (count < k) ? !(bmin < INFINITY) : (T < bmin);
-    const size_t orow = (size_t)jb.out_row + ql;
+    for (int off = 32; off > 0; off >>= 1)
+        T = fminf(T, __shfl_xor(T, off));
+    const uint32_t cnt = (uint32_t)__popcll(__ballot(real && rank < k));
+    const float Bx = lower_bound_exact(B, M.xn[q], M.eps_coef, M.shrink, M.rmax);
+    const bool certified = (cnt < k) ? !(B < INFINITY) : (T < Bx);
     if (!certified) {
-        const uint32_t slot = atomicAdd(M.flag_count, 1u);
-        M.flagged[slot] = make_uint2(mi.job, ql);
+        if (lane == 0) {
+            const uint32_t slot = atomicAdd(M.flag_count, 1u);
+            M.flagged[slot] = make_uint2(mi.job, ql);
+        }
         return;
     }
-#pragma unroll
-    for (int t = 0; t < KM; ++t) {
-        if ((uint32_t)t < k) {
-            const bool ok = bi[t] != NONE;
-            M.out_ids[orow * k + t] = ok ? bi[t] - jb.id_base : NONE;
-            if (M.out_dist)
-                M.out_dist[orow * k + t] = ok ? bd[t] : INFINITY;
-        }
+    const size_t orow = (size_t)jb.out_row + ql;
+    if (mine && rank < k) {
+        M.out_ids[orow * k + rank] = real ? ci - jb.id_base : NONE;
+        if (M.out_dist)
+            M.out_dist[orow * k + rank] = real ? ex : INFINITY;
     }
-    if (M.out_size)
-        M.out_size[orow] = (int32_t)count;
+    if (lane == 0 && M.out_size)
+        M.out_size[orow] = (int32_t)cnt;
 }
 
 // ---------------------------------------------------------------------------
@@ -811,7 +1033,8 @@ struct DevBuf {
 struct Plan {
     std::vector<Job> jobs;
     std::vector<Item> items;
-    std::vector<MergeItem> mitems;
+    std::vector<MergeItem> mitems; // merge: MERGE_ROWS rows per block
+    std::vector<MergeItem> pitems; // packing: MERGE_Q rows per block
     std::vector<uint32_t> seg_start, seg_vend;
     uint64_t part_rows = 0;
     uint64_t pairs = 0;
@@ -864,11 +1087,13 @@ struct ung_hip_ctx {
     ResultBufs group;
     // last group plan (for packing)
     std::vector<Job> group_jobs;
-    std::vector<MergeItem> group_mitems;
+    std::vector<MergeItem> group_pitems;
     DevBuf<Job> gjobs;
     DevBuf<MergeItem> gmitems;
     uint32_t group_list_k = 0;
     DevBuf<uint32_t> graph;
+    // tuning: XCD chunk of the select item order (UNG_HIP_XCD_CHUNK, read at create)
+    uint32_t xcd_chunk = 0;
 };
 
 namespace {
@@ -879,30 +1104,55 @@ int set_device(ung_hip_ctx *ctx)
     return UNG_HIP_OK;
 }
 
+// Candidates per split of a union of u candidates: SPLIT_V, raised (in whole tiles)
+// so that a job never has more than MAX_SPLITS splits.
+uint32_t split_size(uint64_t u)
+{
+    uint64_t s = (u + MAX_SPLITS - 1) / MAX_SPLITS;
+    s = (s + BC - 1) / BC * BC;
+    return (uint32_t)std::max<uint64_t>(SPLIT_V, s);
+}
+
 void add_items_for_job(Plan &pl, uint32_t job_index)
 {
     const Job &jb = pl.jobs[job_index];
-    for (uint32_t qo = 0; qo < jb.q_count; qo += BQ) {
-        const uint32_t qc = std::min<uint32_t>(BQ, jb.q_count - qo);
-        for (uint32_t s = 0; s < jb.n_split; ++s) {
+    // split-major: consecutive items are query blocks streaming the same candidates
+    for (uint32_t s = 0; s < jb.n_split; ++s) {
+        for (uint32_t qo = 0; qo < jb.q_count; qo += BQ) {
+            const uint32_t qc = std::min<uint32_t>(BQ, jb.q_count - qo);
             Item it{};
             it.job = job_index;
             it.q_off = qo;
             it.q_cnt = qc;
-            it.v_begin = s * SPLIT_V;
-            it.v_end = std::min<uint32_t>(jb.n_cand, (s + 1) * SPLIT_V);
+            it.v_begin = s * jb.split_v;
+            it.v_end = (uint32_t)std::min<uint64_t>(jb.n_cand, (uint64_t)(s + 1) * jb.split_v);
             it.split = s;
             pl.items.push_back(it);
             pl.padded += (uint64_t)BQ * (uint64_t)(((it.v_end - it.v_begin) + BC - 1) / BC * BC);
         }
+    }
+    for (uint32_t qo = 0; qo < jb.q_count; qo += MERGE_ROWS) {
+        MergeItem mi{};
+        mi.job = job_index;
+        mi.q_off = qo;
+        mi.q_cnt = std::min<uint32_t>(MERGE_ROWS, jb.q_count - qo);
+        pl.mitems.push_back(mi);
     }
     for (uint32_t qo = 0; qo < jb.q_count; qo += MERGE_Q) {
         MergeItem mi{};
         mi.job = job_index;
         mi.q_off = qo;
         mi.q_cnt = std::min<uint32_t>(MERGE_Q, jb.q_count - qo);
-        pl.mitems.push_back(mi);
+        pl.pitems.push_back(mi);
     }
+}
+
+// Entries per partial row: the k results plus a margin, at most one wave's lanes
+// and at most the 4 queues' entries.
+uint32_t pick_lp(uint32_t k, int lt)
+{
+    const uint32_t margin = std::max<uint32_t>(4u, k / 4);
+    return std::min<uint32_t>(std::min<uint32_t>(64u, 4u * (uint32_t)lt), k + margin);
 }
 
 int pick_lt(uint32_t k)
@@ -915,7 +1165,7 @@ int pick_lt(uint32_t k)
 }
 
 template <int LT>
-int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items)
+int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, bool excl)
 {
     const bool vec4 = (ctx->d % 4) == 0;
     // grid dimension x is limited to 2^31-1; chunk the item list
@@ -924,20 +1174,19 @@ int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items)
         SelectParams Q = P;
         Q.items = P.items + off;
         const uint32_t n = std::min(max_grid, n_items - off);
-        if (vec4)
-            hipLaunchKernelGGL((ung_select_kernel<LT, true>), dim3(n), dim3(NTHREADS), 0, ctx->stream, Q);
+        Q.n_items = n;
+        const uint32_t pad = P.xcd_chunk ? 8u * P.xcd_chunk : 1u;
+        const dim3 g((n + pad - 1) / pad * pad), b(NTHREADS);
+        if (vec4 && excl)
+            hipLaunchKernelGGL((ung_select_kernel<LT, true, true>), g, b, 0, ctx->stream, Q);
+        else if (vec4)
+            hipLaunchKernelGGL((ung_select_kernel<LT, true, false>), g, b, 0, ctx->stream, Q);
+        else if (excl)
+            hipLaunchKernelGGL((ung_select_kernel<LT, false, true>), g, b, 0, ctx->stream, Q);
         else
-            hipLaunchKernelGGL((ung_select_kernel<LT, false>), dim3(n), dim3(NTHREADS), 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, false, false>), g, b, 0, ctx->stream, Q);
         HIPCHECK(hipGetLastError());
     }
-    return UNG_HIP_OK;
-}
-
-template <int KM>
-int launch_merge_t(ung_hip_ctx *ctx, const MergeParams &M, uint32_t n)
-{
-    hipLaunchKernelGGL((ung_merge_kernel<KM>), dim3(n), dim3(MERGE_Q), 0, ctx->stream, M);
-    HIPCHECK(hipGetLastError());
     return UNG_HIP_OK;
 }
 
@@ -946,11 +1195,13 @@ int launch_merge_t(ung_hip_ctx *ctx, const MergeParams &M, uint32_t n)
 int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st)
 {
     int rc;
+    const int lt = pick_lt(k);
+    const uint32_t lp = pick_lp(k, lt);
     const auto t_h2d = clk::now();
     if ((rc = ctx->jobs.ensure(pl.jobs.size())) || (rc = ctx->items.ensure(pl.items.size())) ||
         (rc = ctx->mitems.ensure(pl.mitems.size())) || (rc = ctx->seg_start.ensure(pl.seg_start.size())) ||
         (rc = ctx->seg_vend.ensure(pl.seg_vend.size())) ||
-        (rc = ctx->part_ids.ensure(pl.part_rows * k)) || (rc = ctx->part_dist.ensure(pl.part_rows * k)) ||
+        (rc = ctx->part_ids.ensure(pl.part_rows * lp)) || (rc = ctx->part_dist.ensure(pl.part_rows * lp)) ||
         (rc = ctx->part_bound.ensure(pl.part_rows)) || (rc = ctx->flag_count.ensure(1)) ||
         (rc = ctx->flagged.ensure(std::max<uint64_t>(pl.rows, 1))))
         return rc;
@@ -986,41 +1237,47 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
     P.eps_coef = 2.0 * ((double)ctx->d + 4.0) * std::ldexp(1.0, -24);
     P.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
     P.rmax = ctx->rmax;
-    const int lt = pick_lt(k);
+    P.xcd_chunk = ctx->xcd_chunk;
+    P.lp = lp;
     const uint32_t n_items = (uint32_t)pl.items.size();
+    const bool excl = (pl.jobs[0].flags & 1u) != 0; // one kind of job per plan
     if (lt == 8)
-        rc = launch_select_t<8>(ctx, P, n_items);
+        rc = launch_select_t<8>(ctx, P, n_items, excl);
     else if (lt == 16)
-        rc = launch_select_t<16>(ctx, P, n_items);
+        rc = launch_select_t<16>(ctx, P, n_items, excl);
     else
-        rc = launch_select_t<32>(ctx, P, n_items);
+        rc = launch_select_t<32>(ctx, P, n_items, excl);
     if (rc)
         return rc;
     HIPCHECK(hipEventRecord(ctx->ev[1], ctx->stream));
 
     MergeParams M{};
+    M.X = ctx->X;
+    M.xn = ctx->xn;
+    M.d = ctx->d;
     M.jobs = ctx->jobs.p;
     M.mitems = ctx->mitems.p;
     M.part_ids = ctx->part_ids.p;
     M.part_dist = ctx->part_dist.p;
     M.part_bound = ctx->part_bound.p;
+    M.lp = lp;
     M.k = k;
+    M.eps_coef = P.eps_coef;
+    M.shrink = P.shrink;
+    M.rmax = P.rmax;
     M.out_ids = res.ids.p;
     M.out_dist = res.dist.p;
     M.out_size = res.size.p;
     M.flag_count = ctx->flag_count.p;
     M.flagged = ctx->flagged.p;
     const uint32_t n_m = (uint32_t)pl.mitems.size();
-    if (k <= 8)
-        rc = launch_merge_t<8>(ctx, M, n_m);
-    else if (k <= 16)
-        rc = launch_merge_t<16>(ctx, M, n_m);
-    else if (k <= 32)
-        rc = launch_merge_t<32>(ctx, M, n_m);
-    else
-        rc = launch_merge_t<64>(ctx, M, n_m);
-    if (rc)
-        return rc;
+    for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
+        MergeParams Mc = M;
+        Mc.mitems = M.mitems + off;
+        const uint32_t n = std::min<uint32_t>(1u << 30, n_m - off);
+        hipLaunchKernelGGL(ung_merge_kernel, dim3(n), dim3(64 * MERGE_ROWS), 0, ctx->stream, Mc);
+        HIPCHECK(hipGetLastError());
+    }
     HIPCHECK(hipEventRecord(ctx->ev[2], ctx->stream));
 
     FallbackParams F{};
@@ -1126,7 +1383,8 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
             continue;
         jb.seg_count = (uint32_t)pl.seg_start.size() - jb.seg_begin;
         jb.n_cand = (uint32_t)u;
-        jb.n_split = (uint32_t)((u + SPLIT_V - 1) / SPLIT_V);
+        jb.split_v = split_size(u);
+        jb.n_split = (uint32_t)((u + jb.split_v - 1) / jb.split_v);
         jb.part_base = (uint32_t)pl.part_rows;
         jb.out_row = group_begin[c];
         jb.id_base = 0;
@@ -1217,7 +1475,8 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         pl.seg_start.push_back(grp_begin[g]);
         pl.seg_vend.push_back(n);
         jb.n_cand = n;
-        jb.n_split = (n + SPLIT_V - 1) / SPLIT_V;
+        jb.split_v = split_size(n);
+        jb.n_split = (n + jb.split_v - 1) / jb.split_v;
         jb.part_base = (uint32_t)pl.part_rows;
         jb.out_row = (uint32_t)row;
         jb.id_base = grp_begin[g];
@@ -1246,13 +1505,13 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         return rc;
     // keep the job table for packing
     ctx->group_jobs = pl.jobs;
-    ctx->group_mitems = pl.mitems;
+    ctx->group_pitems = pl.pitems;
     ctx->group_list_k = list_k;
     if (!pl.jobs.empty()) {
-        if ((rc = ctx->gjobs.ensure(pl.jobs.size())) || (rc = ctx->gmitems.ensure(pl.mitems.size())))
+        if ((rc = ctx->gjobs.ensure(pl.jobs.size())) || (rc = ctx->gmitems.ensure(pl.pitems.size())))
             return rc;
         HIPCHECK(hipMemcpyAsync(ctx->gjobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->gmitems.p, pl.mitems.data(), pl.mitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->gmitems.p, pl.pitems.data(), pl.pitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ctx->stream));
     }
     HIPCHECK(hipStreamSynchronize(ctx->stream));
     res.valid = true;
@@ -1359,6 +1618,8 @@ int ung_hip_create(int device, ung_hip_ctx **out)
     HIPCHECK(hipSetDevice(device));
     ung_hip_ctx *ctx = new ung_hip_ctx();
     ctx->device = device;
+    if (const char *s = std::getenv("UNG_HIP_XCD_CHUNK"))
+        ctx->xcd_chunk = (uint32_t)std::min(64L, std::max(0L, std::strtol(s, nullptr, 10)));
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed: %s", hipGetErrorString(e));
@@ -1583,7 +1844,7 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
     const uint64_t rows = ctx->group.rows;
     if ((rc = ctx->graph.ensure(std::max<uint64_t>(rows * stride, 1))))
         return rc;
-    if (!ctx->group_mitems.empty()) {
+    if (!ctx->group_pitems.empty()) {
         PackParams K{};
         K.jobs = ctx->gjobs.p;
         K.mitems = ctx->gmitems.p;
@@ -1598,7 +1859,7 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
         K.graph_stride = stride;
         K.graph = ctx->graph.p;
         HIPCHECK(hipEventRecord(ctx->ev[6], ctx->stream));
-        hipLaunchKernelGGL(ung_pack_kernel, dim3((unsigned)ctx->group_mitems.size()), dim3(MERGE_Q), 0, ctx->stream, K);
+        hipLaunchKernelGGL(ung_pack_kernel, dim3((unsigned)ctx->group_pitems.size()), dim3(MERGE_Q), 0, ctx->stream, K);
         HIPCHECK(hipGetLastError());
         HIPCHECK(hipEventRecord(ctx->ev[7], ctx->stream));
     }
@@ -1610,7 +1871,7 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
         std::memset(entry_points, 0, ctx->group_jobs.size() * sizeof(uint32_t));
     if (st) {
         float kms = 0;
-        if (!ctx->group_mitems.empty())
+        if (!ctx->group_pitems.empty())
             HIPCHECK(hipEventElapsedTime(&kms, ctx->ev[6], ctx->ev[7]));
         st->kernel_ms += kms;
         st->d2h_ms += ms_since(t1);
