@@ -148,12 +148,26 @@ __device__ __forceinline__ float l2_ref_8lane(const float *__restrict__ a,
     return pair + pair_hi;                   // sub 0: (s0+s1)+(s2+s3)
 }
 
-// Same value computed by one lane alone (fallback path).
+// Same value computed by one lane alone.  Rows 16-byte aligned (d % 4 == 0) are read
+// with float4 loads; the accumulation order is the same either way.
 __device__ __forceinline__ float l2_ref_lane(const float *__restrict__ a,
                                              const float *__restrict__ b, uint32_t d)
 {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint32_t p = 0;
+    if ((d & 3u) == 0) {
+        const float4 *a4 = reinterpret_cast<const float4 *>(a);
+        const float4 *b4 = reinterpret_cast<const float4 *>(b);
+        for (; p + 8 <= d; p += 8) {
+            const float4 x0 = a4[p >> 2], x1 = a4[(p >> 2) + 1];
+            const float4 y0 = b4[p >> 2], y1 = b4[(p >> 2) + 1];
+            const float t[8] = {x0.x - y0.x, x0.y - y0.y, x0.z - y0.z, x0.w - y0.w,
+                                x1.x - y1.x, x1.y - y1.y, x1.z - y1.z, x1.w - y1.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l)
+                acc[l] = __builtin_fmaf(t[l], t[l], acc[l]);
+        }
+    }
     for (; p + 8 <= d; p += 8) {
 #pragma unroll
         for (int l = 0; l < 8; ++l) {
@@ -276,28 +290,39 @@ __device__ __forceinline__ int row_of(int wm, int h, int j)
     return wm * 64 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
 }
 
-// acc[j>>4][nb][j&15] for a per-lane index j, as a 5-level select tree over registers.
-__device__ __forceinline__ float select32(const floatx16 (&acc)[2][2], int nb, uint32_t j)
+// lo[j] (j < 16) or hi[j-16] for a per-lane index j, as a 5-level select tree over
+// registers.  The halves come in as vector values, not as an array in memory, so the
+// selects stay register moves (a select between two loads of one local array would
+// be rewritten into an indexed load from scratch memory).
+//
+// Every 2-way select is a byte permute (v_perm_b32 with selector 0x07060504 = first
+// operand, 0x03020100 = second operand): an opaque operation, so the tree is not
+// folded back into a dynamically indexed vector extract (which is lowered through
+// scratch memory).
+__device__ __forceinline__ uint32_t perm_sel(uint32_t j, int bit)
 {
-    float l16[16];
-    const bool b4 = (j & 16u) != 0;
+    return 0x03020100u + ((j >> bit) & 1u) * 0x04040404u;
+}
+
+__device__ __forceinline__ float select32(floatx16 lo, floatx16 hi, uint32_t j)
+{
+    const uint32_t s4 = perm_sel(j, 4), s0 = perm_sel(j, 0), s1 = perm_sel(j, 1);
+    const uint32_t s2 = perm_sel(j, 2), s3 = perm_sel(j, 3);
+    uint32_t l16[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-        l16[i] = b4 ? acc[1][nb][i] : acc[0][nb][i];
-    float l8[8];
-    const bool b0 = (j & 1u) != 0;
+        l16[i] = __builtin_amdgcn_perm(__float_as_uint(hi[i]), __float_as_uint(lo[i]), s4);
+    uint32_t l8[8];
 #pragma unroll
     for (int a = 0; a < 8; ++a)
-        l8[a] = b0 ? l16[2 * a + 1] : l16[2 * a];
-    float l4[4];
-    const bool b1 = (j & 2u) != 0;
+        l8[a] = __builtin_amdgcn_perm(l16[2 * a + 1], l16[2 * a], s0);
+    uint32_t l4[4];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-        l4[a] = b1 ? l8[2 * a + 1] : l8[2 * a];
-    const bool b2 = (j & 4u) != 0, b3 = (j & 8u) != 0;
-    const float l2a = b2 ? l4[1] : l4[0];
-    const float l2b = b2 ? l4[3] : l4[2];
-    return b3 ? l2b : l2a;
+        l4[a] = __builtin_amdgcn_perm(l8[2 * a + 1], l8[2 * a], s1);
+    const uint32_t l2a = __builtin_amdgcn_perm(l4[1], l4[0], s2);
+    const uint32_t l2b = __builtin_amdgcn_perm(l4[3], l4[2], s2);
+    return __uint_as_float(__builtin_amdgcn_perm(l2b, l2a, s3));
 }
 
 // Pre-filter bound in s-space: s = |x|^2/2 - <x,q> and a = fl(2s + |q|^2).  Returns c
@@ -545,7 +570,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                     if (m != 0u) {
                         const uint32_t j = (uint32_t)__builtin_clz(m);
                         m &= ~(0x80000000u >> j);
-                        const float dd = __builtin_fmaf(2.0f, select32(acc, nb, j), qnv[nb]);
+                        const float dd = __builtin_fmaf(2.0f, select32(acc[0][nb], acc[1][nb], j), qnv[nb]);
                         if (dd < fminf(ld[nb][LT - 1], tsh[nb])) {
                             list_insert<LT>(ld[nb], li[nb], dd, sm.rowid[slot][row_of(wm, h, (int)j)]);
                             tsh[nb] = fminf(tsh[nb], ld[nb][LT - 1]);
@@ -599,39 +624,44 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                 sm.u.r.alist[jl][lid] = fminf(ld[nb][LT - 1], tfin[nb]);
             }
         }
-        if (tid < 64)
-            sm.u.r.drop[tid] = INFINITY;
         __syncthreads();
-        // rank of every entry under (approx, id, slot)
-        for (int p = tid; p < rows_here * E; p += NTHREADS) {
-            const int jl = p / E, e = p % E;
-            const uint32_t ql = (uint32_t)(pass * 64 + jl);
-            const float de = sm.u.r.ed[jl][e];
-            const uint32_t ie = sm.u.r.ei[jl][e];
-            uint32_t rank = 0;
-            for (int f = 0; f < E; ++f) {
-                const float df = sm.u.r.ed[jl][f];
-                const uint32_t idf = sm.u.r.ei[jl][f];
-                rank += (df < de || (df == de && (idf < ie || (idf == ie && f < e)))) ? 1u : 0u;
-            }
-            const size_t prow = (size_t)jb.part_base + (size_t)it.split * jb.q_count + it.q_off + ql;
-            if (rank < Lp) {
-                const bool real = ie != NONE && de < INFINITY;
-                P.part_ids[prow * Lp + rank] = real ? ie : NONE;
-                P.part_dist[prow * Lp + rank] = real ? de : INFINITY;
-            } else if (rank == Lp) {
-                sm.u.r.drop[jl] = de; // smallest queued value left out of the partial row
-            }
-        }
-        __syncthreads();
+        // one thread per query: 4-way merge of the sorted queues -> approximate top-Lp;
+        // the first value left out joins the bound
         if (tid < rows_here) {
             const int jl = tid;
             const uint32_t ql = (uint32_t)(pass * 64 + jl);
-            float A = sm.u.r.drop[jl];
+            const size_t prow = (size_t)jb.part_base + (size_t)it.split * jb.q_count + it.q_off + ql;
+            int hp[4] = {0, 0, 0, 0};
+            float drop = INFINITY;
+            for (uint32_t t = 0; t <= Lp; ++t) {
+                float bd = INFINITY;
+                uint32_t bi = NONE;
+                int bl = -1;
+#pragma unroll
+                for (int l = 0; l < 4; ++l) {
+                    if (hp[l] < LT) {
+                        const float dl = sm.u.r.ed[jl][l * LT + hp[l]];
+                        const uint32_t il = sm.u.r.ei[jl][l * LT + hp[l]];
+                        if (il != NONE && cand_less(dl, il, bd, bi)) {
+                            bd = dl;
+                            bi = il;
+                            bl = l;
+                        }
+                    }
+                }
+                if (t == Lp) {
+                    drop = bd;
+                    break;
+                }
+                P.part_ids[prow * Lp + t] = bi;
+                P.part_dist[prow * Lp + t] = bd;
+                if (bl >= 0)
+                    ++hp[bl];
+            }
+            float A = drop;
 #pragma unroll
             for (int l = 0; l < 4; ++l)
                 A = fminf(A, sm.u.r.alist[jl][l]);
-            const size_t prow = (size_t)jb.part_base + (size_t)it.split * jb.q_count + it.q_off + ql;
             P.part_bound[prow] = A; // approximate-distance space
         }
     }
@@ -674,63 +704,61 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
     const uint32_t q = jb.q_begin + ql;
     const uint32_t S = jb.n_split, Lp = M.lp, k = M.k;
 
-    size_t prow = 0;
-    uint32_t pos = 0;
-    float hd = INFINITY, bnd = INFINITY;
-    uint32_t hi = NONE;
-    if ((uint32_t)lane < S) {
-        prow = (size_t)jb.part_base + (size_t)lane * jb.q_count + ql;
-        bnd = M.part_bound[prow];
-        hd = M.part_dist[prow * Lp];
-        hi = M.part_ids[prow * Lp];
-    }
-    float bmin = bnd;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        bmin = fminf(bmin, __shfl_xor(bmin, off));
-
-    // lane t < Lp receives the t-th smallest approximate candidate
-    float a_next = INFINITY;
-    uint32_t ci = NONE;
-    for (uint32_t t = 0; t <= Lp; ++t) {
-        float bd = hd;
-        uint32_t bi = hi;
-        wave_argmin(bd, bi);
-        if (bi == NONE)
-            break; // every head is exhausted (uniform)
-        if (t == Lp) {
-            a_next = bd;
-            break;
+    uint32_t ci = NONE; // lane t < Lp: the t-th smallest approximate candidate
+    float B;            // approximate-space bound of every candidate left out
+    if (S == 1) {
+        // one split: its partial row is already the approximate top-Lp
+        const size_t prow = (size_t)jb.part_base + ql;
+        if ((uint32_t)lane < Lp)
+            ci = M.part_ids[prow * Lp + lane];
+        B = M.part_bound[prow];
+    } else {
+        size_t prow = 0;
+        uint32_t pos = 0;
+        float hd = INFINITY, bnd = INFINITY;
+        uint32_t hi = NONE;
+        if ((uint32_t)lane < S) {
+            prow = (size_t)jb.part_base + (size_t)lane * jb.q_count + ql;
+            bnd = M.part_bound[prow];
+            hd = M.part_dist[prow * Lp];
+            hi = M.part_ids[prow * Lp];
         }
-        if ((uint32_t)lane == t)
-            ci = bi;
-        if (hi == bi) {
-            ++pos;
-            if (pos < Lp) {
-                hd = M.part_dist[prow * Lp + pos];
-                hi = M.part_ids[prow * Lp + pos];
-            } else {
-                hd = INFINITY;
-                hi = NONE;
+        float bmin = bnd;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            bmin = fminf(bmin, __shfl_xor(bmin, off));
+        float a_next = INFINITY;
+        for (uint32_t t = 0; t <= Lp; ++t) {
+            float bd = hd;
+            uint32_t bi = hi;
+            wave_argmin(bd, bi);
+            if (bi == NONE)
+                break; // every head is exhausted (uniform)
+            if (t == Lp) {
+                a_next = bd;
+                break;
+            }
+            if ((uint32_t)lane == t)
+                ci = bi;
+            if (hi == bi) {
+                ++pos;
+                if (pos < Lp) {
+                    hd = M.part_dist[prow * Lp + pos];
+                    hi = M.part_ids[prow * Lp + pos];
+                } else {
+                    hd = INFINITY;
+                    hi = NONE;
+                }
             }
         }
+        B = fminf(bmin, a_next);
     }
-    const float B = fminf(bmin, a_next); // approximate-space bound of everything left out
 
-    // exact re-score: 8 groups of 8 lanes, candidate e = base + group
-    const int sub = lane & 7, grp = lane >> 3;
+    // exact re-score, one lane per candidate
     const float *qv = M.X + (size_t)q * M.d;
     float ex = INFINITY;
-    for (uint32_t base = 0; base < Lp; base += 8) {
-        const uint32_t e = base + (uint32_t)grp;
-        const uint32_t id = __shfl(ci, (int)(e < 64u ? e : 63u));
-        float v = INFINITY;
-        if (e < Lp && id != NONE) // uniform inside the 8-lane group
-            v = l2_ref_8lane(qv, M.X + (size_t)id * M.d, M.d, sub);
-        const float got = __shfl(v, (int)((((uint32_t)lane - base) & 7u) * 8u));
-        if ((uint32_t)lane >= base && (uint32_t)lane < base + 8u)
-            ex = got;
-    }
+    if (ci != NONE)
+        ex = l2_ref_lane(qv, M.X + (size_t)ci * M.d, M.d);
     // rank under (exact, id, lane)
     uint32_t rank = 0;
     for (uint32_t f = 0; f < Lp; ++f) {
@@ -1155,11 +1183,12 @@ uint32_t pick_lp(uint32_t k, int lt)
     return std::min<uint32_t>(std::min<uint32_t>(64u, 4u * (uint32_t)lt), k + margin);
 }
 
+// Queue length: k <= LT lets the 4 queues of a query share thresholds.
 int pick_lt(uint32_t k)
 {
-    if (k <= 16)
+    if (k <= 8)
         return 8;
-    if (k <= 32)
+    if (k <= 16)
         return 16;
     return 32;
 }
