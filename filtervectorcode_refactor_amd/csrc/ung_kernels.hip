@@ -213,6 +213,35 @@ __device__ __forceinline__ void list_insert(float (&ld)[LT], uint32_t (&li)[LT],
     }
 }
 
+// Ascending bitonic sort of a 32-entry register queue (dist keys, ids carried along);
+// all indices are compile-time constants, so the network stays in registers.
+template <int LT>
+__device__ __forceinline__ void bitonic_sort32(float (&ld)[LT], uint32_t (&li)[LT])
+{
+    if constexpr (LT == 32) {
+#pragma unroll
+        for (int k = 2; k <= 32; k <<= 1) {
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int l = i ^ j;
+                    if (l > i) {
+                        const bool up = (i & k) == 0;
+                        const bool sw = up ? (ld[l] < ld[i]) : (ld[i] < ld[l]);
+                        const float a = ld[i], b = ld[l];
+                        const uint32_t ia = li[i], ib = li[l];
+                        ld[i] = sw ? b : a;
+                        ld[l] = sw ? a : b;
+                        li[i] = sw ? ib : ia;
+                        li[l] = sw ? ia : ib;
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Lower bound on the exact (reference-rounded) distance of any candidate whose
 // expansion-form MFMA distance is >= A:
 //   |a - D| <= eps_coef * (|q| + R)^2   (norm cache, MFMA dot, epilogue roundings)
@@ -566,6 +595,21 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 uint32_t m = pend[nb];
+                if (LT == 32 && tile == 0) {
+                    // first tile with empty 32-entry queues: the tile's 32 candidates
+                    // are the queue; sort them in registers (bitonic network) instead
+                    // of 32 insertion rounds
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) {
+                        const float sv = acc[j >> 4][nb][j & 15];
+                        const float dd = __builtin_fmaf(2.0f, sv, qnv[nb]);
+                        ld[nb][j & (LT - 1)] = dd;
+                        li[nb][j & (LT - 1)] = dd < INFINITY ? sm.rowid[slot][row_of(wm, h, j)] : NONE;
+                    }
+                    bitonic_sort32<LT>(ld[nb], li[nb]);
+                    tsh[nb] = fminf(tsh[nb], ld[nb][LT - 1]);
+                    m = 0u;
+                }
                 while (__ballot(m != 0u)) {
                     if (m != 0u) {
                         const uint32_t j = (uint32_t)__builtin_clz(m);
