@@ -17,6 +17,7 @@ Prints ONE JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -50,6 +51,23 @@ def read_traffic():
                 except ValueError:
                     return None
     return None
+
+
+def calib_copy(nbytes):
+    """One device-to-device hipMemcpy of nbytes (the runtime's blit kernel): the
+    reference reading for FETCH_SIZE / WRITE_SIZE in a rocprofv3 --pmc pass."""
+    hip = C.CDLL("libamdhip64.so")
+    src, dst = C.c_void_p(), C.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(C.byref(p), C.c_size_t(nbytes)) != 0:
+            raise RuntimeError("hipMalloc failed in calib_copy")
+    try:
+        if hip.hipMemcpy(dst, src, C.c_size_t(nbytes), 3) != 0 or hip.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipMemcpy failed in calib_copy")
+    finally:
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    log(f"calibration copy {nbytes} bytes done")
 
 
 def cpu_baseline(st, k, seconds=12.0, threads=None):
@@ -103,6 +121,8 @@ def main():
     ap.add_argument("--n", type=int, default=0, help="override point count (smaller runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="end with a 1 GiB device-to-device copy (counter calibration for --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (one-GPU boxes); "
@@ -165,7 +185,7 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_FP32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
                 "traffic": traffic,
-                "kernel": "ung_select_kernel<8,true> (cross edges, one launch per step)",
+                "kernel": "ung_select_kernel<8,true,false> (cross edges, one launch per step)",
                 "flops_per_launch": flops_cross, "avg_launch_ms": round(sel_cross_ms, 4)}
     value = (p_cross + p_intra) / (ms_per_step * 1e-3)
     result = {
@@ -202,6 +222,8 @@ def main():
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(st, cfg.k_cross, seconds=args.cpu_seconds)
     st.close()
+    if args.calib_copy:
+        calib_copy(1 << 30)
     print(json.dumps(result), flush=True)
 
 

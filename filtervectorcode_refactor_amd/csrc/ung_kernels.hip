@@ -86,6 +86,7 @@ struct SelectParams {
     uint32_t n_items; // items of this launch
     uint32_t xcd_chunk; // XCD chunking of the item order (0 = identity)
     uint32_t lp;      // entries per partial row (approximate top-Lp)
+    uint32_t x_bytes; // bytes of X (buffer range of the 32-bit-offset kernels)
 };
 
 // ---------------------------------------------------------------------------
@@ -197,49 +198,23 @@ __device__ __forceinline__ float l2_ref_lane(const float *__restrict__ a,
 }
 #pragma clang fp contract(on)
 
+// Sorted insert of (nd, ni) into an ascending register queue (ties keep the older
+// entry first; nd = +inf changes nothing).  Runs from the tail so every entry is
+// updated in place from the old values of itself and its predecessor.
 template <int LT>
 __device__ __forceinline__ void list_insert(float (&ld)[LT], uint32_t (&li)[LT], float nd,
                                             uint32_t ni)
 {
+    bool c_hi = nd < ld[LT - 1];
 #pragma unroll
-    for (int j = 0; j < LT; ++j) {
-        const bool sw = nd < ld[j];
-        const float td = ld[j];
-        const uint32_t ti = li[j];
-        ld[j] = sw ? nd : td;
-        li[j] = sw ? ni : ti;
-        nd = sw ? td : nd;
-        ni = sw ? ti : ni;
+    for (int j = LT - 1; j > 0; --j) {
+        const bool c_lo = nd < ld[j - 1];
+        ld[j] = c_hi ? (c_lo ? ld[j - 1] : nd) : ld[j];
+        li[j] = c_hi ? (c_lo ? li[j - 1] : ni) : li[j];
+        c_hi = c_lo;
     }
-}
-
-// Ascending bitonic sort of a 32-entry register queue (dist keys, ids carried along);
-// all indices are compile-time constants, so the network stays in registers.
-template <int LT>
-__device__ __forceinline__ void bitonic_sort32(float (&ld)[LT], uint32_t (&li)[LT])
-{
-    if constexpr (LT == 32) {
-#pragma unroll
-        for (int k = 2; k <= 32; k <<= 1) {
-#pragma unroll
-            for (int j = k >> 1; j > 0; j >>= 1) {
-#pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    const int l = i ^ j;
-                    if (l > i) {
-                        const bool up = (i & k) == 0;
-                        const bool sw = up ? (ld[l] < ld[i]) : (ld[i] < ld[l]);
-                        const float a = ld[i], b = ld[l];
-                        const uint32_t ia = li[i], ib = li[l];
-                        ld[i] = sw ? b : a;
-                        ld[l] = sw ? a : b;
-                        li[i] = sw ? ib : ia;
-                        li[l] = sw ? ia : ib;
-                    }
-                }
-            }
-        }
-    }
+    ld[0] = c_hi ? nd : ld[0];
+    li[0] = c_hi ? ni : li[0];
 }
 
 // Lower bound on the exact (reference-rounded) distance of any candidate whose
@@ -291,11 +266,15 @@ struct alignas(16) SelectSmem {
             float drop[64];      // smallest queued value not written to the partial row
         } r;
     } u;
-    uint32_t rowid[3][BC]; // candidate ids of tiles t%3 (ring: built one tile ahead)
-    float4 xnr[3][BC / 4]; // their half squared norms (+inf for padding rows), 4 rows per float4
+    uint32_t rowid[3][BC]; // candidate ids of tiles t%3 (ring: built one tile ahead; NONE = padding)
+    float4 nhx[3][BC / 4]; // their -|x|^2/2 (-inf for padding rows), 4 rows per float4
     float qn[BQ];
     float tau[2][2][BQ];   // [tile parity][candidate wave][query]: a wave's queue threshold
 };
+static_assert(BQ == BC, "the epilogue staging addresses assume square panels");
+// flat float offsets inside SelectSmem::u.p
+constexpr int PANEL_X = 2 * BQ * LDSW; // start of xs relative to qs
+constexpr int ROW32 = 32 * LDSW;       // 32 panel rows
 
 // Logical work item of a block.  Blocks are dispatched round-robin over the 8 XCDs
 // (blockIdx % 8).  With chunk c > 0 the logical items are cut into chunks of c
@@ -310,48 +289,6 @@ __device__ __forceinline__ uint32_t xcd_logical_block(uint32_t b, uint32_t n, ui
     const uint32_t x = b & 7u, j = b >> 3;
     const uint32_t L = ((j / c) * 8u + x) * c + (j % c);
     return L < n ? L : NONE;
-}
-
-// Tile row of a lane's j-th value of one query column (j = 16*mb + i of acc[mb][nb][i]).
-__device__ __forceinline__ int row_of(int wm, int h, int j)
-{
-    const int mb = j >> 4, i = j & 15;
-    return wm * 64 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-}
-
-// lo[j] (j < 16) or hi[j-16] for a per-lane index j, as a 5-level select tree over
-// registers.  The halves come in as vector values, not as an array in memory, so the
-// selects stay register moves (a select between two loads of one local array would
-// be rewritten into an indexed load from scratch memory).
-//
-// Every 2-way select is a byte permute (v_perm_b32 with selector 0x07060504 = first
-// operand, 0x03020100 = second operand): an opaque operation, so the tree is not
-// folded back into a dynamically indexed vector extract (which is lowered through
-// scratch memory).
-__device__ __forceinline__ uint32_t perm_sel(uint32_t j, int bit)
-{
-    return 0x03020100u + ((j >> bit) & 1u) * 0x04040404u;
-}
-
-__device__ __forceinline__ float select32(floatx16 lo, floatx16 hi, uint32_t j)
-{
-    const uint32_t s4 = perm_sel(j, 4), s0 = perm_sel(j, 0), s1 = perm_sel(j, 1);
-    const uint32_t s2 = perm_sel(j, 2), s3 = perm_sel(j, 3);
-    uint32_t l16[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-        l16[i] = __builtin_amdgcn_perm(__float_as_uint(hi[i]), __float_as_uint(lo[i]), s4);
-    uint32_t l8[8];
-#pragma unroll
-    for (int a = 0; a < 8; ++a)
-        l8[a] = __builtin_amdgcn_perm(l16[2 * a + 1], l16[2 * a], s0);
-    uint32_t l4[4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-        l4[a] = __builtin_amdgcn_perm(l8[2 * a + 1], l8[2 * a], s1);
-    const uint32_t l2a = __builtin_amdgcn_perm(l4[1], l4[0], s2);
-    const uint32_t l2b = __builtin_amdgcn_perm(l4[3], l4[2], s2);
-    return __uint_as_float(__builtin_amdgcn_perm(l2b, l2a, s3));
 }
 
 // Pre-filter bound in s-space: s = |x|^2/2 - <x,q> and a = fl(2s + |q|^2).  Returns c
@@ -377,11 +314,127 @@ __device__ __forceinline__ void build_rowids(SelectSmem &sm, int slot, const Sel
             nx = P.xn[g];
         }
         sm.rowid[slot][tid] = g;
-        reinterpret_cast<float *>(sm.xnr[slot])[tid] = 0.5f * nx; // |x|^2/2 (exact scaling)
+        reinterpret_cast<float *>(sm.nhx[slot])[tid] = -0.5f * nx; // -|x|^2/2 (exact scaling)
     }
 }
 
-template <int LT, bool VEC4, bool EXCL>
+// Tile row (0..127) of a lane's j-th value of one query column, j = 16*mb + i of
+// acc[mb][nb][i]:  wm*64 + mb*32 + 8*(i/4) + 4*h + i%4.
+__device__ __forceinline__ uint32_t tile_row(int wm, int h, uint32_t j)
+{
+    return (uint32_t)(wm * 64 + 4 * h) + ((j & 28u) << 1) + (j & 3u);
+}
+
+// Index j of tile row offset o = row - (wm*64 + 4*h) when the row belongs to the lane
+// (0 <= o < 64 and bit 2 of o clear), else 32.
+__device__ __forceinline__ uint32_t lane_index_of(int o)
+{
+    return (o >= 0 && o < 64 && (o & 4) == 0) ? (((uint32_t)o >> 1) & 28u) | ((uint32_t)o & 3u) : 32u;
+}
+
+// Compare-exchange of entries a < b of a register queue (ascending by distance).  The
+// swap mask is the sign of d[b] - d[a] (all ones iff d[b] < d[a] for the non-negative,
+// possibly infinite distances here; inf - inf gives a NaN that swaps two +inf entries
+// at most), applied with bit selects, so no lane-mask registers stay live across the
+// interleaved exchanges of a network.
+__device__ __forceinline__ uint32_t bitsel(uint32_t m, uint32_t a, uint32_t b)
+{
+    return (a & m) | (b & ~m);
+}
+
+template <int N>
+__device__ __forceinline__ void cas(float (&d)[N], uint32_t (&id)[N], int a, int b)
+{
+    const uint32_t da = __float_as_uint(d[a]), db = __float_as_uint(d[b]);
+    const uint32_t m = (uint32_t)((int32_t)__float_as_uint(d[b] - d[a]) >> 31);
+    d[a] = __uint_as_float(bitsel(m, db, da));
+    d[b] = __uint_as_float(bitsel(m, da, db));
+    const uint32_t ia = id[a], ib = id[b];
+    id[a] = bitsel(m, ib, ia);
+    id[b] = bitsel(m, ia, ib);
+}
+
+// Ascending bitonic sort of the 8 entries at base..base+7 (24 compare-exchanges).
+template <int N>
+__device__ __forceinline__ void sort8(float (&d)[N], uint32_t (&id)[N], int base)
+{
+#pragma unroll
+    for (int k = 2; k <= 8; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    if ((i & k) == 0)
+                        cas(d, id, base + i, base + l);
+                    else
+                        cas(d, id, base + l, base + i);
+                }
+            }
+}
+
+// The 8 smallest of two ascending 8-runs at a and b, ascending, into the run at a
+// (half cleaner on a[i] vs b[7-i], then a bitonic merge of the 8 kept).
+template <int N>
+__device__ __forceinline__ void merge8_keep(float (&d)[N], uint32_t (&id)[N], int a, int b)
+{
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int l = b + 7 - i;
+        const uint32_t m = (uint32_t)((int32_t)__float_as_uint(d[l] - d[a + i]) >> 31);
+        d[a + i] = __uint_as_float(bitsel(m, __float_as_uint(d[l]), __float_as_uint(d[a + i])));
+        id[a + i] = bitsel(m, id[l], id[a + i]);
+    }
+#pragma unroll
+    for (int j = 4; j > 0; j >>= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int l = i ^ j;
+            if (l > i)
+                cas(d, id, a + i, a + l);
+        }
+}
+
+// Ascending queue of the LT smallest of 32 (dist, id) entries: the first tile of an
+// item fills its empty queues with a sorting network instead of 32 insertions.
+template <int LT>
+__device__ __forceinline__ void best_of_32(float (&d)[32], uint32_t (&id)[32], float (&ld)[LT], uint32_t (&li)[LT])
+{
+    if constexpr (LT == 8) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            sort8(d, id, 8 * g);
+        merge8_keep(d, id, 0, 8);
+        merge8_keep(d, id, 16, 24);
+        merge8_keep(d, id, 0, 16);
+    } else {
+#pragma unroll
+        for (int k = 2; k <= 32; k <<= 1)
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int l = i ^ j;
+                    if (l > i) {
+                        if ((i & k) == 0)
+                            cas(d, id, i, l);
+                        else
+                            cas(d, id, l, i);
+                    }
+                }
+    }
+#pragma unroll
+    for (int j = 0; j < LT; ++j) {
+        ld[j] = d[j];
+        li[j] = id[j];
+    }
+}
+
+// FAST: d % 4 == 0 and X smaller than 4 GiB -- 16-byte buffer loads with 32-bit byte
+// offsets (the k-chunk advances a scalar offset, so the main loop spends no vector ALU
+// work on addresses).  Otherwise 64-bit pointers with per-element bounds.
+template <int LT, bool FAST, bool EXCL>
 __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
 {
     __shared__ SelectSmem sm;
@@ -420,23 +473,27 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     // loader mapping: rows lr = (tid>>3) + 32m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
     const int c4 = (tid & 7) * 4;
-    const float *qrow[4];
+    [[maybe_unused]] __amdgpu_buffer_rsrc_t xres;
+    [[maybe_unused]] uint32_t qoff[4], xoff[4];
+    [[maybe_unused]] const float *qrow[4];
+    [[maybe_unused]] const float *xrow[4];
+    if constexpr (FAST)
+        xres = __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, (int)P.x_bytes, 0x00020000);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         uint32_t ql = (uint32_t)(lr0 + 32 * m);
         ql = ql < qcnt ? ql : qcnt - 1;
-        qrow[m] = X + (size_t)(q0 + ql) * d;
+        if constexpr (FAST)
+            qoff[m] = ((q0 + ql) * d + (uint32_t)c4) * 4u;
+        else
+            qrow[m] = X + (size_t)(q0 + ql) * d;
     }
 
     __syncthreads();
-    uint32_t qid[2];
     float qnv[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int ql = wn * 64 + nb * 32 + r;
-        qid[nb] = q0 + (uint32_t)ql;
-        qnv[nb] = sm.qn[ql];
-    }
+    for (int nb = 0; nb < 2; ++nb)
+        qnv[nb] = sm.qn[wn * 64 + nb * 32 + r];
 
     // One flat software pipeline over (candidate tile, k-chunk) steps: the panels are
     // double-buffered in LDS and each step prefetches the next step's chunk (also
@@ -446,29 +503,42 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     const uint32_t nk = (d + KC - 1) / KC;
     const uint32_t total = ntiles * nk;
 
-    const float *xrow[4];
     auto set_xrows = [&](int slot) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             uint32_t g = sm.rowid[slot][lr0 + 32 * m];
-            g = (g == NONE) ? sm.rowid[slot][0] : g;
-            xrow[m] = X + (size_t)g * d;
+            g = (g == NONE) ? 0u : g; // padding rows load row 0 (their -|x|^2/2 is -inf)
+            if constexpr (FAST)
+                xoff[m] = (g * d + (uint32_t)c4) * 4u;
+            else
+                xrow[m] = X + (size_t)g * d;
         }
     };
     float4 rq[4], rx[4];
     auto load_chunk = [&](uint32_t kc) {
-        const uint32_t col = kc + (uint32_t)c4;
+        if constexpr (FAST) {
+            if (kc + KC <= d) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            if (VEC4) {
-                if (col < d) {
-                    rq[m] = *reinterpret_cast<const float4 *>(qrow[m] + col);
-                    rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + col);
-                } else {
+                for (int m = 0; m < 4; ++m) {
+                    rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m], kc * 4u, 0));
+                    rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
+                }
+            } else { // ragged last chunk (d % 32 != 0): columns >= d read as zero
+                const bool ok = kc + (uint32_t)c4 < d;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
                     rq[m] = make_float4(0.f, 0.f, 0.f, 0.f);
                     rx[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (ok) {
+                        rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m] + kc * 4u, 0, 0));
+                        rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m] + kc * 4u, 0, 0));
+                    }
                 }
-            } else {
+            }
+        } else {
+            const uint32_t col = kc + (uint32_t)c4;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
                 float tq[4], tx[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
@@ -482,16 +552,27 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         }
     };
 
+    // accumulators start at -|x|^2/2 of their row, so after the k-loop
+    // acc = <x,q> - |x|^2/2 = -s  with  s = |x|^2/2 - <x,q>  (padding rows: -inf)
     floatx16 acc[2][2];
+    auto init_acc = [&](int slot) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const float4 v = sm.nhx[slot][(wm * 64 + mb * 32 + 8 * g4 + 4 * h) >> 2];
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                acc[a][b][i] = 0.0f;
+                for (int nb = 0; nb < 2; ++nb) {
+                    acc[mb][nb][4 * g4 + 0] = v.x;
+                    acc[mb][nb][4 * g4 + 1] = v.y;
+                    acc[mb][nb][4 * g4 + 2] = v.z;
+                    acc[mb][nb][4 * g4 + 3] = v.w;
+                }
+            }
+    };
 
     __syncthreads(); // ring slot 0 and qn visible
+    init_acc(0);
     set_xrows(0);
     load_chunk(0);
 
@@ -542,16 +623,16 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
             build_rowids(sm, next_slot, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
 
         if (kc + 1 == nk) {
-            // epilogue: acc[mb][nb][i] = <x_row, q_col>, row = wm*64+mb*32+8*(i/4)+4*h+(i%4),
-            // col = wn*64+nb*32+r.  s = |x|^2/2 - <x,q> and the expansion-form distance is
-            // a = fl(2s + |q|^2) (padding rows: |x|^2 = +inf).
+            // epilogue: acc[mb][nb][i] = -s for row tile_row(wm, h, 16*mb + i) and query
+            // col = wn*64+nb*32+r, s = |x|^2/2 - <x,q>; the expansion-form distance is
+            // a = fl(2s + |q|^2) = fma(-2, acc, |q|^2) (padding rows: acc = -inf).
             //
             // The four queues of a query (lane halves h, candidate waves wm) share a
             // threshold: a candidate is queued only if a < min(own LT-th, partner lane's,
             // other wave's of the previous tile).  Any candidate with a >= that value can
             // not be among the query's LT best (one queue already holds LT better ones),
             // and thresholds only decrease, so a stale value is safe.
-            float tsh[2], cth[2];
+            float tsh[2], ncth[2];
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 const int col = wn * 64 + nb * 32 + r;
@@ -564,71 +645,91 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                         t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col]);
                 }
                 tsh[nb] = t;
-                cth[nb] = s_bound(t, qnv[nb]);
+                ncth[nb] = -s_bound(t, qnv[nb]);
             }
-            // branch-free pass: s in place of acc, and per list a lane mask whose bit
-            // (31 - j) marks element j under the pre-filter bound
+            // branch-free pass: per list a lane mask whose bit (31 - j) marks element j
+            // under the pre-filter bound (s < c  <=>  the sign bit of -c - acc; a NaN
+            // from -inf - -inf only marks a padding row, which the round rejects)
             uint32_t pend[2] = {0u, 0u};
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-                float4 xq[4];
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4)
-                    xq[g4] = sm.xnr[slot][(wm * 64 + mb * 32 + 8 * g4 + 4 * h) >> 2];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float4 x4 = xq[i >> 2];
-                    const float hxv = (i & 3) == 0 ? x4.x : (i & 3) == 1 ? x4.y : (i & 3) == 2 ? x4.z : x4.w;
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb) {
-                        float sv = hxv - acc[mb][nb][i];
-                        if (EXCL) {
-                            const int row = wm * 64 + mb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                            sv = sm.rowid[slot][row] == qid[nb] ? INFINITY : sv;
-                        }
-                        acc[mb][nb][i] = sv;
-                        pend[nb] = (pend[nb] << 1) | (sv < cth[nb] ? 1u : 0u);
-                    }
-                }
-            }
-            // rounds: each lane inserts at most one pending element per list per round
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                uint32_t m = pend[nb];
-                if (LT == 32 && tile == 0) {
-                    // first tile with empty 32-entry queues: the tile's 32 candidates
-                    // are the queue; sort them in registers (bitonic network) instead
-                    // of 32 insertion rounds
-#pragma unroll
-                    for (int j = 0; j < 32; ++j) {
-                        const float sv = acc[j >> 4][nb][j & 15];
-                        const float dd = __builtin_fmaf(2.0f, sv, qnv[nb]);
-                        ld[nb][j & (LT - 1)] = dd;
-                        li[nb][j & (LT - 1)] = dd < INFINITY ? sm.rowid[slot][row_of(wm, h, j)] : NONE;
-                    }
-                    bitonic_sort32<LT>(ld[nb], li[nb]);
-                    tsh[nb] = fminf(tsh[nb], ld[nb][LT - 1]);
-                    m = 0u;
-                }
-                while (__ballot(m != 0u)) {
-                    if (m != 0u) {
-                        const uint32_t j = (uint32_t)__builtin_clz(m);
-                        m &= ~(0x80000000u >> j);
-                        const float dd = __builtin_fmaf(2.0f, select32(acc[0][nb], acc[1][nb], j), qnv[nb]);
-                        if (dd < fminf(ld[nb][LT - 1], tsh[nb])) {
-                            list_insert<LT>(ld[nb], li[nb], dd, sm.rowid[slot][row_of(wm, h, (int)j)]);
-                            tsh[nb] = fminf(tsh[nb], ld[nb][LT - 1]);
-                        }
-                    }
-                }
-            }
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb)
+                for (int i = 0; i < 16; ++i)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        acc[mb][nb][i] = 0.0f;
+                    for (int nb = 0; nb < 2; ++nb)
+                        pend[nb] = (pend[nb] << 1) | (__float_as_uint(ncth[nb] - acc[mb][nb][i]) >> 31);
+            // self exclusion (candidate space = query space): clear the query's own bit
+            uint32_t self_j[2] = {32u, 32u};
+            if constexpr (EXCL) {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    const int o = (int)(it.q_off + (uint32_t)(wn * 64 + nb * 32 + r)) -
+                                  (int)(it.v_begin + tile * BC) - (wm * 64 + 4 * h);
+                    self_j[nb] = lane_index_of(o);
+                    pend[nb] &= self_j[nb] < 32u ? ~(0x80000000u >> self_j[nb]) : 0xFFFFFFFFu;
+                }
+            }
+            // Each thread owns the 8 panel slots it fills at the next step (buffer buf^1,
+            // read by no wave before the next barrier): one list's 32 values are staged
+            // there, so a round reads its element with one LDS load instead of a register
+            // select tree.  Slot g holds values 4g..4g+3.
+            float *const pnl = reinterpret_cast<float *>(&sm.u.p);
+            const int own0 = ((buf ^ 1) * BQ + lr0) * LDSW + c4;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                for (int g = 0; g < 8; ++g) {
+                    const int mb = g >> 2, g4 = g & 3;
+                    const float4 v = make_float4(acc[mb][nb][4 * g4], acc[mb][nb][4 * g4 + 1],
+                                                 acc[mb][nb][4 * g4 + 2], acc[mb][nb][4 * g4 + 3]);
+                    *reinterpret_cast<float4 *>(pnl + own0 + mb * PANEL_X + g4 * ROW32) = v;
+                }
+                uint32_t m = pend[nb];
+                if (tile == 0) {
+                    // first tile: the queues are empty; a sorting network keeps the LT best
+                    // of the tile's 32 candidates instead of up to 32 insertion rounds
+                    float dv[32];
+                    uint32_t iv[32];
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) {
+                        const uint4 ids = *reinterpret_cast<const uint4 *>(&sm.rowid[slot][tile_row(wm, h, 4u * g)]);
+                        const uint32_t idg[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * g + e;
+                            float dd = __builtin_fmaf(-2.0f, acc[j >> 4][nb][j & 15], qnv[nb]);
+                            if constexpr (EXCL)
+                                dd = (uint32_t)j == self_j[nb] ? INFINITY : dd;
+                            dv[j] = dd;
+                            iv[j] = dd < INFINITY ? idg[e] : NONE;
+                        }
+                    }
+                    best_of_32<LT>(dv, iv, ld[nb], li[nb]);
+                    m = 0u;
+                }
+                // rounds: each lane inserts at most one pending element per round; the
+                // body is branch-free (an idle lane inserts +inf, which changes nothing)
+                // and the round count is the wave's largest pending count
+                // (binary search on ballots: wave-uniform, no cross-lane data movement)
+                const uint32_t np = (uint32_t)__popc(m);
+                uint32_t nr = 0;
+#pragma unroll
+                for (int b = 5; b >= 0; --b) {
+                    const uint32_t c = nr | (1u << b);
+                    if (__ballot(np >= c))
+                        nr = c;
+                }
+                for (uint32_t rr = 0; rr < nr; ++rr) {
+                    const uint32_t j = (uint32_t)__builtin_clz(m | 1u);
+                    const bool act = m != 0u;
+                    m &= ~(0x80000000u >> j);
+                    const float av = pnl[own0 + (int)(j >> 4) * PANEL_X + (int)((j >> 2) & 3u) * ROW32 + (int)(j & 3u)];
+                    const uint32_t rid = sm.rowid[slot][tile_row(wm, h, j)];
+                    float dd = __builtin_fmaf(-2.0f, av, qnv[nb]);
+                    dd = (act && dd < fminf(ld[nb][LT - 1], tsh[nb])) ? dd : INFINITY;
+                    list_insert<LT>(ld[nb], li[nb], dd, rid);
+                }
+            }
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 // publish this wave's threshold of the query for the other wave
@@ -638,6 +739,8 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                 if (share && h == 0)
                     sm.tau[tile & 1][wm][wn * 64 + nb * 32 + r] = pair_t;
             }
+            if (tile + 1 < ntiles)
+                init_acc(next_slot);
             ++tile;
             kc = 0;
             slot = next_slot;
@@ -1240,19 +1343,22 @@ int pick_lt(uint32_t k)
 template <int LT>
 int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, bool excl)
 {
-    const bool vec4 = (ctx->d % 4) == 0;
+    // 32-bit buffer offsets need 16-byte rows inside a < 4 GiB base set
+    const uint64_t x_bytes = (uint64_t)ctx->N * ctx->d * sizeof(float);
+    const bool fast = (ctx->d % 4) == 0 && x_bytes < (1ull << 32);
     // grid dimension x is limited to 2^31-1; chunk the item list
     const uint32_t max_grid = 1u << 30;
     for (uint32_t off = 0; off < n_items; off += max_grid) {
         SelectParams Q = P;
         Q.items = P.items + off;
+        Q.x_bytes = fast ? (uint32_t)x_bytes : 0u;
         const uint32_t n = std::min(max_grid, n_items - off);
         Q.n_items = n;
         const uint32_t pad = P.xcd_chunk ? 8u * P.xcd_chunk : 1u;
         const dim3 g((n + pad - 1) / pad * pad), b(NTHREADS);
-        if (vec4 && excl)
+        if (fast && excl)
             hipLaunchKernelGGL((ung_select_kernel<LT, true, true>), g, b, 0, ctx->stream, Q);
-        else if (vec4)
+        else if (fast)
             hipLaunchKernelGGL((ung_select_kernel<LT, true, false>), g, b, 0, ctx->stream, Q);
         else if (excl)
             hipLaunchKernelGGL((ung_select_kernel<LT, false, true>), g, b, 0, ctx->stream, Q);
