@@ -84,7 +84,7 @@ struct SelectParams {
     double shrink;    // (d/8+8)*2^-24 : relative error of the reference summation
     double rmax;      // max candidate norm (slightly inflated)
     uint32_t n_items; // items of this launch
-    uint32_t xcd_chunk; // XCD chunking of the item order (0 = identity)
+    uint32_t *item_ctr; // next item to take (zeroed before the launch)
     uint32_t lp;      // entries per partial row (approximate top-Lp)
     uint32_t x_bytes; // bytes of X (buffer range of the 32-bit-offset kernels)
 };
@@ -276,19 +276,18 @@ static_assert(BQ == BC, "the epilogue staging addresses assume square panels");
 constexpr int PANEL_X = 2 * BQ * LDSW; // start of xs relative to qs
 constexpr int ROW32 = 32 * LDSW;       // 32 panel rows
 
-// Logical work item of a block.  Blocks are dispatched round-robin over the 8 XCDs
-// (blockIdx % 8).  With chunk c > 0 the logical items are cut into chunks of c
-// consecutive items -- query blocks of one job that stream the same candidate
-// rows -- and chunk i runs on XCD i % 8, so a chunk shares one L2 while the chunks
-// stay interleaved across XCDs for balance.  The grid is padded to a multiple of
-// 8c; returns NONE for padding blocks.  c = 0: identity.
-__device__ __forceinline__ uint32_t xcd_logical_block(uint32_t b, uint32_t n, uint32_t c)
+// Work item of a block, taken from a launch-wide counter when the block starts.  The
+// hardware deals blocks to the 8 XCDs and to their shader engines round-robin by
+// block index, a fixed share each; with item costs from 1 to 128 tiles a fixed share
+// leaves engines idle while others still work.  Taking the next item (items sorted
+// by decreasing cost) when a block actually starts balances the engines.  The grid
+// has exactly n_items blocks, so every block gets one distinct item.
+__device__ __forceinline__ uint32_t take_item(uint32_t *ctr, uint32_t *slot)
 {
-    if (c == 0)
-        return b;
-    const uint32_t x = b & 7u, j = b >> 3;
-    const uint32_t L = ((j / c) * 8u + x) * c + (j % c);
-    return L < n ? L : NONE;
+    if (threadIdx.x == 0)
+        *slot = atomicAdd(ctr, 1u);
+    __syncthreads();
+    return *slot;
 }
 
 // Pre-filter bound in s-space: s = |x|^2/2 - <x,q> and a = fl(2s + |q|^2).  Returns c
@@ -438,8 +437,9 @@ template <int LT, bool FAST, bool EXCL>
 __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
 {
     __shared__ SelectSmem sm;
-    const uint32_t logical = xcd_logical_block(blockIdx.x, P.n_items, P.xcd_chunk);
-    if (logical == NONE)
+    __shared__ uint32_t item_slot;
+    const uint32_t logical = take_item(P.item_ctr, &item_slot);
+    if (logical >= P.n_items)
         return;
     const Item it = P.items[logical];
     const Job jb = P.jobs[it.job];
@@ -1267,8 +1267,6 @@ struct ung_hip_ctx {
     DevBuf<MergeItem> gmitems;
     uint32_t group_list_k = 0;
     DevBuf<uint32_t> graph;
-    // tuning: XCD chunk of the select item order (UNG_HIP_XCD_CHUNK, read at create)
-    uint32_t xcd_chunk = 0;
 };
 
 namespace {
@@ -1354,8 +1352,11 @@ int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, b
         Q.x_bytes = fast ? (uint32_t)x_bytes : 0u;
         const uint32_t n = std::min(max_grid, n_items - off);
         Q.n_items = n;
-        const uint32_t pad = P.xcd_chunk ? 8u * P.xcd_chunk : 1u;
-        const dim3 g((n + pad - 1) / pad * pad), b(NTHREADS);
+        if (off > 0) { // the counter was zeroed for the first chunk by the caller
+            hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ctx->stream, P.item_ctr, 1u);
+            HIPCHECK(hipGetLastError());
+        }
+        const dim3 g(n), b(NTHREADS);
         if (fast && excl)
             hipLaunchKernelGGL((ung_select_kernel<LT, true, true>), g, b, 0, ctx->stream, Q);
         else if (fast)
@@ -1381,12 +1382,18 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
         (rc = ctx->mitems.ensure(pl.mitems.size())) || (rc = ctx->seg_start.ensure(pl.seg_start.size())) ||
         (rc = ctx->seg_vend.ensure(pl.seg_vend.size())) ||
         (rc = ctx->part_ids.ensure(pl.part_rows * lp)) || (rc = ctx->part_dist.ensure(pl.part_rows * lp)) ||
-        (rc = ctx->part_bound.ensure(pl.part_rows)) || (rc = ctx->flag_count.ensure(1)) ||
+        (rc = ctx->part_bound.ensure(pl.part_rows)) || (rc = ctx->flag_count.ensure(2)) ||
         (rc = ctx->flagged.ensure(std::max<uint64_t>(pl.rows, 1))))
         return rc;
+    // select items in order of decreasing cost (candidate tiles); the stable sort keeps
+    // the query blocks of one split next to each other
+    std::vector<Item> order(pl.items);
+    std::stable_sort(order.begin(), order.end(), [](const Item &a, const Item &b) {
+        return (a.v_end - a.v_begin + BC - 1) / BC > (b.v_end - b.v_begin + BC - 1) / BC;
+    });
     if (!pl.jobs.empty()) {
         HIPCHECK(hipMemcpyAsync(ctx->jobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->items.p, pl.items.data(), pl.items.size() * sizeof(Item), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->items.p, order.data(), order.size() * sizeof(Item), hipMemcpyHostToDevice, ctx->stream));
         HIPCHECK(hipMemcpyAsync(ctx->mitems.p, pl.mitems.data(), pl.mitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ctx->stream));
         HIPCHECK(hipMemcpyAsync(ctx->seg_start.p, pl.seg_start.data(), pl.seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
         HIPCHECK(hipMemcpyAsync(ctx->seg_vend.p, pl.seg_vend.data(), pl.seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
@@ -1397,7 +1404,8 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
     if (pl.jobs.empty())
         return UNG_HIP_OK;
 
-    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->flag_count.p, 1u);
+    // flag_count[0]: rows flagged for the fallback, [1]: select item counter
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->flag_count.p, 2u);
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipEventRecord(ctx->ev[0], ctx->stream));
 
@@ -1416,7 +1424,7 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
     P.eps_coef = 2.0 * ((double)ctx->d + 4.0) * std::ldexp(1.0, -24);
     P.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
     P.rmax = ctx->rmax;
-    P.xcd_chunk = ctx->xcd_chunk;
+    P.item_ctr = ctx->flag_count.p + 1;
     P.lp = lp;
     const uint32_t n_items = (uint32_t)pl.items.size();
     const bool excl = (pl.jobs[0].flags & 1u) != 0; // one kind of job per plan
@@ -1797,8 +1805,6 @@ int ung_hip_create(int device, ung_hip_ctx **out)
     HIPCHECK(hipSetDevice(device));
     ung_hip_ctx *ctx = new ung_hip_ctx();
     ctx->device = device;
-    if (const char *s = std::getenv("UNG_HIP_XCD_CHUNK"))
-        ctx->xcd_chunk = (uint32_t)std::min(64L, std::max(0L, std::strtol(s, nullptr, 10)));
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed: %s", hipGetErrorString(e));
