@@ -3,14 +3,13 @@
 //
 // Path (one call = one "job list"):
 //   select  : fused fp32 MFMA distance tiles (v_mfma_f32_32x32x2f32, LDS-staged
-//             query/candidate panels) with a per-row register top-LT queue in the
-//             epilogue -- no distance matrix ever reaches HBM.  At the end of a
-//             work item the queued candidates are re-scored EXACTLY in the
-//             reference's summation order and the k best are written as a partial
-//             row together with a certified lower bound on every candidate that
-//             was not queued.
-//   merge   : per result row, merges the partial rows of its candidate splits and
-//             certifies that no unqueued candidate can enter the top-k.
+//             query/candidate panels) with per-row register queues in the epilogue
+//             -- no distance matrix ever reaches HBM.  At the end of a work item the
+//             approximate (expansion-form) top-Lp of every query is written as a
+//             partial row with a bound that every candidate left out satisfies.
+//   merge   : per result row, merges the partial rows of its candidate splits,
+//             re-scores the Lp best EXACTLY in the reference's summation order and
+//             certifies that no candidate left out can enter the top-k.
 //   fallback: rows whose bound does not certify the result are rescanned exactly
 //             (rare; counted in ung_hip_stats::fallback_rows).
 //
