@@ -429,10 +429,16 @@ __device__ __forceinline__ void best_of_32(float (&d)[32], uint32_t (&id)[32], f
     }
 }
 
-// FAST: d % 4 == 0 and X smaller than 4 GiB -- 16-byte buffer loads with 32-bit byte
-// offsets (the k-chunk advances a scalar offset, so the main loop spends no vector ALU
-// work on addresses).  Otherwise 64-bit pointers with per-element bounds.
-template <int LT, bool FAST, bool EXCL>
+// Operand loads (d % 4 == 0 for the two 16-byte modes):
+//   LOAD_BUF32 : X smaller than 4 GiB -- buffer loads with 32-bit byte offsets; the
+//                k-chunk advances a scalar offset, so the main loop spends no vector ALU
+//                work on addresses;
+//   LOAD_WIDE  : larger X -- queries through a buffer based at the item's first query
+//                row, candidates through 64-bit row pointers (one add per load);
+//   LOAD_SCALAR: any d -- 64-bit pointers with per-element bounds.
+enum : int { LOAD_SCALAR = 0, LOAD_BUF32 = 1, LOAD_WIDE = 2 };
+
+template <int LT, int MODE, bool EXCL>
 __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
 {
     __shared__ SelectSmem sm;
@@ -472,18 +478,24 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     // loader mapping: rows lr = (tid>>3) + 32m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
     const int c4 = (tid & 7) * 4;
-    [[maybe_unused]] __amdgpu_buffer_rsrc_t xres;
+    [[maybe_unused]] __amdgpu_buffer_rsrc_t qres, xres;
     [[maybe_unused]] uint32_t qoff[4], xoff[4];
     [[maybe_unused]] const float *qrow[4];
     [[maybe_unused]] const float *xrow[4];
-    if constexpr (FAST)
+    if constexpr (MODE == LOAD_BUF32) {
         xres = __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, (int)P.x_bytes, 0x00020000);
+    } else if constexpr (MODE == LOAD_WIDE) {
+        qres = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)q0 * d), (short)0, (int)(qcnt * d * 4u),
+                                                 0x00020000);
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         uint32_t ql = (uint32_t)(lr0 + 32 * m);
         ql = ql < qcnt ? ql : qcnt - 1;
-        if constexpr (FAST)
+        if constexpr (MODE == LOAD_BUF32)
             qoff[m] = ((q0 + ql) * d + (uint32_t)c4) * 4u;
+        else if constexpr (MODE == LOAD_WIDE)
+            qoff[m] = (ql * d + (uint32_t)c4) * 4u;
         else
             qrow[m] = X + (size_t)(q0 + ql) * d;
     }
@@ -507,20 +519,27 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         for (int m = 0; m < 4; ++m) {
             uint32_t g = sm.rowid[slot][lr0 + 32 * m];
             g = (g == NONE) ? 0u : g; // padding rows load row 0 (their -|x|^2/2 is -inf)
-            if constexpr (FAST)
+            if constexpr (MODE == LOAD_BUF32)
                 xoff[m] = (g * d + (uint32_t)c4) * 4u;
+            else if constexpr (MODE == LOAD_WIDE)
+                xrow[m] = X + (size_t)g * d + c4;
             else
                 xrow[m] = X + (size_t)g * d;
         }
     };
     float4 rq[4], rx[4];
     auto load_chunk = [&](uint32_t kc) {
-        if constexpr (FAST) {
+        if constexpr (MODE != LOAD_SCALAR) {
             if (kc + KC <= d) {
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                    rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m], kc * 4u, 0));
-                    rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
+                    if constexpr (MODE == LOAD_BUF32) {
+                        rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m], kc * 4u, 0));
+                        rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
+                    } else {
+                        rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff[m], kc * 4u, 0));
+                        rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + kc);
+                    }
                 }
             } else { // ragged last chunk (d % 32 != 0): columns >= d read as zero
                 const bool ok = kc + (uint32_t)c4 < d;
@@ -529,8 +548,13 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                     rq[m] = make_float4(0.f, 0.f, 0.f, 0.f);
                     rx[m] = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (ok) {
-                        rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m] + kc * 4u, 0, 0));
-                        rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m] + kc * 4u, 0, 0));
+                        if constexpr (MODE == LOAD_BUF32) {
+                            rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m] + kc * 4u, 0, 0));
+                            rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m] + kc * 4u, 0, 0));
+                        } else {
+                            rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff[m] + kc * 4u, 0, 0));
+                            rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + kc);
+                        }
                     }
                 }
             }
@@ -1023,24 +1047,31 @@ __global__ __launch_bounds__(64) void ung_fallback_kernel(FallbackParams F)
 // ---------------------------------------------------------------------------
 // small kernels
 // ---------------------------------------------------------------------------
-__global__ void ung_norm_kernel(const float *__restrict__ X, uint64_t N, uint32_t d,
-                                float *__restrict__ xn, unsigned int *__restrict__ maxbits)
+// Squared norms (one wave per row, grid-stride over rows; lanes stride the row) and the
+// largest of them: a block-wide maximum, then one atomic per block.
+__global__ __launch_bounds__(256) void ung_norm_kernel(const float *__restrict__ X, uint64_t N, uint32_t d,
+                                                       float *__restrict__ xn, unsigned int *__restrict__ maxbits)
 {
-    // one wave per row; lanes stride the row
-    const uint64_t row = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= N)
-        return;
-    const float *x = X + row * d;
-    float s = 0.0f;
-    for (uint32_t t = lane; t < d; t += 64)
-        s = __builtin_fmaf(x[t], x[t], s);
-    for (int off = 32; off > 0; off >>= 1)
-        s += __shfl_xor(s, off);
-    if (lane == 0) {
-        xn[row] = s;
-        atomicMax(maxbits, __float_as_uint(s)); // non-negative floats order as uints
+    __shared__ unsigned int wmax[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t nwaves = (uint64_t)gridDim.x * 4u;
+    unsigned int mx = 0u; // non-negative floats order as their bit patterns
+    for (uint64_t row = (uint64_t)blockIdx.x * 4u + (uint64_t)wave; row < N; row += nwaves) {
+        const float *x = X + row * d;
+        float s = 0.0f;
+        for (uint32_t t = lane; t < d; t += 64)
+            s = __builtin_fmaf(x[t], x[t], s);
+        for (int off = 32; off > 0; off >>= 1)
+            s += __shfl_xor(s, off);
+        if (lane == 0)
+            xn[row] = s;
+        mx = max(mx, __float_as_uint(s));
     }
+    if (lane == 0)
+        wmax[wave] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        atomicMax(maxbits, max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3])));
 }
 
 __global__ void ung_fill_rows_kernel(uint32_t *ids, float *dist, int32_t *size, uint64_t rows,
@@ -1266,6 +1297,8 @@ struct ung_hip_ctx {
     DevBuf<MergeItem> gmitems;
     uint32_t group_list_k = 0;
     DevBuf<uint32_t> graph;
+    // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
+    bool force_wide = false;
 };
 
 namespace {
@@ -1340,15 +1373,17 @@ int pick_lt(uint32_t k)
 template <int LT>
 int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, bool excl)
 {
-    // 32-bit buffer offsets need 16-byte rows inside a < 4 GiB base set
+    // 16-byte loads need d % 4 == 0; 32-bit buffer offsets a base set below 4 GiB
     const uint64_t x_bytes = (uint64_t)ctx->N * ctx->d * sizeof(float);
-    const bool fast = (ctx->d % 4) == 0 && x_bytes < (1ull << 32);
+    const int mode = (ctx->d % 4) != 0                                  ? LOAD_SCALAR
+                     : (x_bytes < (1ull << 32) && !ctx->force_wide) ? LOAD_BUF32
+                                                                      : LOAD_WIDE;
     // grid dimension x is limited to 2^31-1; chunk the item list
     const uint32_t max_grid = 1u << 30;
     for (uint32_t off = 0; off < n_items; off += max_grid) {
         SelectParams Q = P;
         Q.items = P.items + off;
-        Q.x_bytes = fast ? (uint32_t)x_bytes : 0u;
+        Q.x_bytes = mode == LOAD_BUF32 ? (uint32_t)x_bytes : 0u;
         const uint32_t n = std::min(max_grid, n_items - off);
         Q.n_items = n;
         if (off > 0) { // the counter was zeroed for the first chunk by the caller
@@ -1356,14 +1391,18 @@ int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, b
             HIPCHECK(hipGetLastError());
         }
         const dim3 g(n), b(NTHREADS);
-        if (fast && excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, true, true>), g, b, 0, ctx->stream, Q);
-        else if (fast)
-            hipLaunchKernelGGL((ung_select_kernel<LT, true, false>), g, b, 0, ctx->stream, Q);
+        if (mode == LOAD_BUF32 && excl)
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true>), g, b, 0, ctx->stream, Q);
+        else if (mode == LOAD_BUF32)
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false>), g, b, 0, ctx->stream, Q);
+        else if (mode == LOAD_WIDE && excl)
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true>), g, b, 0, ctx->stream, Q);
+        else if (mode == LOAD_WIDE)
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false>), g, b, 0, ctx->stream, Q);
         else if (excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, false, true>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_SCALAR, true>), g, b, 0, ctx->stream, Q);
         else
-            hipLaunchKernelGGL((ung_select_kernel<LT, false, false>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_SCALAR, false>), g, b, 0, ctx->stream, Q);
         HIPCHECK(hipGetLastError());
     }
     return UNG_HIP_OK;
@@ -1752,9 +1791,9 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
     HIPCHECK(hipStreamSynchronize(ctx->stream));
     const double h2d = ms_since(t0);
     HIPCHECK(hipEventRecord(ctx->ev[4], ctx->stream));
-    const uint32_t rows_per_block = 4;
-    hipLaunchKernelGGL(ung_norm_kernel, dim3((unsigned)((N + rows_per_block - 1) / rows_per_block)), dim3(64 * rows_per_block),
-                       0, ctx->stream, ctx->X, N, dim, ctx->xn, ctx->maxbits);
+    const uint64_t norm_blocks = std::min<uint64_t>((N + 3) / 4, 8192);
+    hipLaunchKernelGGL(ung_norm_kernel, dim3((unsigned)norm_blocks), dim3(256), 0, ctx->stream, ctx->X, N, dim,
+                       ctx->xn, ctx->maxbits);
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipEventRecord(ctx->ev[5], ctx->stream));
     unsigned int mb = 0;
@@ -1804,6 +1843,8 @@ int ung_hip_create(int device, ung_hip_ctx **out)
     HIPCHECK(hipSetDevice(device));
     ung_hip_ctx *ctx = new ung_hip_ctx();
     ctx->device = device;
+    if (const char *s = std::getenv("UNG_HIP_FORCE_WIDE"))
+        ctx->force_wide = s[0] == '1';
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed: %s", hipGetErrorString(e));

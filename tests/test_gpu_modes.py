@@ -1,0 +1,128 @@
+"""GPU parity of the other operand-load modes and of cfg2 at its full size.
+
+* The > 4 GiB load mode (queries through an item-based buffer, candidates through
+  64-bit row pointers) forced at small sizes with UNG_HIP_FORCE_WIDE=1, bit-exact
+  against the oracle.
+* cfg2 at its full size (1M x 128): a random sample of cross-edge rows and of mid
+  groups compared bit-exactly with the reference's own compiled distance + queue
+  (oracle/_ref, else the plain-C oracle), plus size-independent properties of every
+  row (sorted by (dist, id), ids inside the row's minimum-superset union, sizes).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import filtervectorcode_refactor_amd as F
+from filtervectorcode_refactor_amd import datasets as D
+from test_gpu_parity import _assert_rows_equal, _two_level_problem
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def wide_ctx():
+    old = os.environ.get("UNG_HIP_FORCE_WIDE")
+    os.environ["UNG_HIP_FORCE_WIDE"] = "1"
+    try:
+        c = F.HipContext(0)
+    finally:
+        if old is None:
+            del os.environ["UNG_HIP_FORCE_WIDE"]
+        else:
+            os.environ["UNG_HIP_FORCE_WIDE"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("dim,k,seed", [(128, 6, 21), (12, 6, 22), (768, 20, 23), (36, 1, 24)])
+def test_wide_cross(wide_ctx, oracle, dim, k, seed):
+    print(f"wide cross dim={dim} k={k}", flush=True)
+    rng = np.random.default_rng(seed)
+    X, gb, op, oi = _two_level_problem(rng, [1, 3, 130, 300, 7], [4, 200, 2, 129, 5], dim, dup=True)
+    wide_ctx.prepare_vectors(X)
+    ids, dist, size, _ = wide_ctx.cross_topk(gb, op, oi, k)
+    ip, ii = F.in_neighbors(op, oi)
+    o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, k)
+    _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, f"wide dim={dim} k={k}")
+
+
+@pytest.mark.parametrize("n,list_k,dim", [(129, 32, 128), (700, 32, 384), (300, 8, 20)])
+def test_wide_intra(wide_ctx, oracle, n, list_k, dim):
+    print(f"wide intra n={n} k={list_k} dim={dim}", flush=True)
+    rng = np.random.default_rng(n + dim)
+    X = rng.standard_normal((n + 7, dim)).astype(np.float32)
+    X[5] = X[3]
+    wide_ctx.prepare_vectors(X)
+    ids, dist, _ = wide_ctx.group_knn([3], [n], list_k)
+    oi, od = oracle.intra_exact(X, 3, n, list_k)
+    _assert_rows_equal(ids, dist, None, oi, od, None, f"wide intra n={n}")
+
+
+def _checker(oracle):
+    from oracle import RefOracle, ref_available
+    return RefOracle() if ref_available() else oracle
+
+
+def test_cfg2_full_size(oracle):
+    cfg = D.CONFIGS["cfg2"]
+    print("cfg2 full: generate", flush=True)
+    X, lp, li = D.generate(cfg)
+    st = F.UngBuildStage(num_cross_edges=6, max_degree=32)
+    st.prepare_inputs(X, lp, li)
+    del X
+    ctx = st.ctx
+    ctx.prepare_vectors(st.base)
+    print("cfg2 full: cross", flush=True)
+    ids, dist, size, stats = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+    assert stats["fallback_rows"] == 0
+    N = st.base.shape[0]
+    sizes = np.diff(st.group_begin.astype(np.int64))[1:]
+    out_cnt = np.diff(st.out_ptr.astype(np.int64))[1:]
+    union = np.zeros(st.num_groups + 1, np.int64)
+    for c in np.nonzero(out_cnt)[0] + 1:
+        xs = st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]].astype(np.int64)
+        union[c] = int(sizes[xs - 1].sum())
+    pg = st.new_vec_id_to_group_id
+    # sizes and padding, every row
+    assert np.array_equal(size, np.minimum(6, union[pg]).astype(np.int32))
+    valid = np.arange(6)[None, :] < size[:, None]
+    assert ((ids == 0xFFFFFFFF) == ~valid).all()
+    # (dist, id) order, every row
+    d0, d1 = dist[:, :-1], dist[:, 1:]
+    i0, i1 = ids[:, :-1], ids[:, 1:]
+    both = valid[:, 1:]
+    assert ((d0 < d1) | ((d0 == d1) & (i0 < i1)) | ~both).all()
+    # ids inside the union of the row's minimum supersets, every row
+    gid = np.where(valid, pg[np.minimum(ids, N - 1)], 0)
+    for c in np.nonzero(out_cnt)[0] + 1:
+        rows = slice(int(st.group_begin[c]), int(st.group_begin[c + 1]))
+        allowed = np.zeros(st.num_groups + 1, bool)
+        allowed[st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]]] = True
+        g = gid[rows][valid[rows]]
+        assert allowed[g].all(), f"group {c}: id outside its union"
+    # bit-exact against the reference on a random sample of rows
+    chk = _checker(oracle)
+    rng = np.random.default_rng(5)
+    eligible = np.nonzero(union[pg] > 0)[0].astype(np.uint32)
+    q = np.sort(rng.choice(eligible, size=min(6000, eligible.size), replace=False)).astype(np.uint32)
+    print(f"cfg2 full: reference check of {q.size} rows", flush=True)
+    res = chk.cross_exact_points(st.base, st.group_begin, pg, st.out_ptr, st.out_idx, q, 6)
+    _assert_rows_equal(ids[q], dist[q], None, res[0], res[1], None, "cfg2 full cross sample")
+    # intra: a sample of mid groups, bit-exact
+    gids = st.mid_groups()
+    pick = rng.choice(gids, size=min(12, len(gids)), replace=False)
+    begins = st.group_begin[gids]
+    gsz = st.group_begin[gids + 1] - begins
+    print(f"cfg2 full: intra {len(gids)} groups", flush=True)
+    kids, kdist, kstats = ctx.group_knn(begins, gsz, 32)
+    assert kstats["fallback_rows"] == 0
+    starts = np.zeros(len(gids), np.int64)
+    starts[1:] = np.cumsum(gsz.astype(np.int64))[:-1]
+    row_of = dict(zip(gids.tolist(), starts.tolist()))
+    for g in pick:
+        b, n = int(st.group_begin[g]), int(st.group_begin[g + 1] - st.group_begin[g])
+        o_i, o_d = chk.intra_exact(st.base, b, n, 32)
+        r0 = row_of[int(g)]
+        _assert_rows_equal(kids[r0: r0 + n], kdist[r0: r0 + n], None, o_i, o_d, None, f"cfg2 full intra {g}")
+    st.close()
