@@ -1094,6 +1094,41 @@ __global__ void ung_zero_u32_kernel(uint32_t *p, uint32_t n)
         p[i] = 0;
 }
 
+// Group id (1..G) of every point, from the group-contiguous ranges.
+__global__ void ung_point_group_kernel(const uint32_t *__restrict__ group_begin, uint32_t G,
+                                       uint32_t *__restrict__ pg)
+{
+    for (uint32_t g = blockIdx.x + 1; g <= G; g += gridDim.x)
+        for (uint32_t i = group_begin[g] + threadIdx.x; i < group_begin[g + 1]; i += blockDim.x)
+            pg[i] = g;
+}
+
+// Additional edges, step 1 (src/uni_nav_graph_cross_edges.cpp:489-531): marks every entry
+// p of the LNG row of C = group(i) whose group is reached by one of the first `use` cross
+// edges of point i.  One thread per point; entries only ever go 0 -> 1.
+__global__ void ung_addl_mark_kernel(const uint32_t *__restrict__ ids, uint32_t stride, uint32_t use,
+                                     const uint32_t *__restrict__ pg, uint64_t N,
+                                     const uint32_t *__restrict__ out_ptr, const uint32_t *__restrict__ out_idx,
+                                     uint32_t *__restrict__ reached)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= N)
+        return;
+    const uint32_t c = pg[i];
+    const uint32_t b = out_ptr[c], e = out_ptr[c + 1];
+    for (uint32_t t = 0; t < use && b < e; ++t) {
+        const uint32_t nb = ids[i * stride + t];
+        if (nb == NONE)
+            continue;
+        const uint32_t x = pg[nb];
+        for (uint32_t p = b; p < e; ++p)
+            if (out_idx[p] == x) {
+                reached[p] = 1u;
+                break;
+            }
+    }
+}
+
 // Exact-anchor row packing (src/tagore_graph_builder.cu:727-794), one thread per row.
 struct PackParams {
     const Job *jobs;
@@ -1297,6 +1332,9 @@ struct ung_hip_ctx {
     DevBuf<MergeItem> gmitems;
     uint32_t group_list_k = 0;
     DevBuf<uint32_t> graph;
+    // additional edges: group ranges, LNG rows, point groups, reached flags, result rows
+    DevBuf<uint32_t> a_gb, a_op, a_oi, a_pg, a_reached, a_ids;
+    DevBuf<int32_t> a_size;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
     bool force_wide = false;
 };
@@ -1745,6 +1783,197 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
     return UNG_HIP_OK;
 }
 
+// Additional edges (src/uni_nav_graph_cross_edges.cpp:442-596, exact branch :543-562)
+// from the resident cross-edge rows: reached out-groups are marked on the device, the
+// missing (C, X) pairs become one job each (C's first m vectors against X's range, m
+// vectors of min(|X|, num_cross/2) edges each until num_cross are reached), scored
+// exactly by the fallback kernel, and compacted into per-group edge lists on the host.
+int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
+                      const uint32_t *out_idx, uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
+                      uint32_t *edge_to, uint64_t capacity, uint64_t *n_edges, ung_hip_stats *st)
+{
+    int rc;
+    if ((rc = check_ready(ctx)))
+        return rc;
+    if (!ctx->cross.valid) {
+        set_error("ung_hip_additional_edges: no cross-edge result on the device (run ung_hip_cross_topk first)");
+        return UNG_HIP_ESTATE;
+    }
+    if (num_cross < 1 || num_cross > ctx->cross.k) {
+        set_error("ung_hip_additional_edges: num_cross=%u outside 1..%u (the k of the cross-edge call)", num_cross,
+                  ctx->cross.k);
+        return UNG_HIP_EINVAL;
+    }
+    if (!group_begin || !out_ptr || !edge_ptr || !n_edges || (out_ptr[G + 1] > 0 && !out_idx)) {
+        set_error("ung_hip_additional_edges: null argument");
+        return UNG_HIP_EINVAL;
+    }
+    if ((uint64_t)group_begin[G + 1] != ctx->N) {
+        set_error("ung_hip_additional_edges: group_begin[G+1]=%u but %llu vectors are prepared", group_begin[G + 1],
+                  (unsigned long long)ctx->N);
+        return UNG_HIP_EINVAL;
+    }
+    for (uint32_t g = 1; g <= G; ++g)
+        if (group_begin[g + 1] < group_begin[g] || out_ptr[g + 1] < out_ptr[g]) {
+            set_error("ung_hip_additional_edges: group_begin/out_ptr not monotone at group %u", g);
+            return UNG_HIP_EINVAL;
+        }
+    const uint32_t E = out_ptr[G + 1];
+    for (uint32_t p = 0; p < E; ++p)
+        if (out_idx[p] < 1 || out_idx[p] > G) {
+            set_error("ung_hip_additional_edges: out_idx entry %u out of range 1..%u", out_idx[p], G);
+            return UNG_HIP_EINVAL;
+        }
+    if ((rc = set_device(ctx)))
+        return rc;
+    const auto t0 = clk::now();
+    const uint64_t N = ctx->N;
+    const uint32_t per_max = num_cross / 2;
+    std::vector<uint32_t> reached(E, 0u);
+    if (E > 0 && per_max > 0) {
+        if ((rc = ctx->a_gb.ensure(G + 2)) || (rc = ctx->a_op.ensure(G + 2)) || (rc = ctx->a_oi.ensure(E)) ||
+            (rc = ctx->a_pg.ensure(N)) || (rc = ctx->a_reached.ensure(E)))
+            return rc;
+        HIPCHECK(hipMemcpyAsync(ctx->a_gb.p, group_begin, (G + 2) * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->a_op.p, out_ptr, (G + 2) * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->a_oi.p, out_idx, E * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        hipLaunchKernelGGL(ung_zero_u32_kernel, dim3((E + 255) / 256), dim3(256), 0, ctx->stream, ctx->a_reached.p, E);
+        HIPCHECK(hipGetLastError());
+        hipLaunchKernelGGL(ung_point_group_kernel, dim3(std::max<uint32_t>(1u, std::min<uint32_t>(G, 65535u))), dim3(256),
+                           0, ctx->stream, ctx->a_gb.p, G, ctx->a_pg.p);
+        HIPCHECK(hipGetLastError());
+        hipLaunchKernelGGL(ung_addl_mark_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, ctx->stream,
+                           ctx->cross.ids.p, ctx->cross.k, num_cross, ctx->a_pg.p, N, ctx->a_op.p, ctx->a_oi.p,
+                           ctx->a_reached.p);
+        HIPCHECK(hipGetLastError());
+        HIPCHECK(hipMemcpyAsync(reached.data(), ctx->a_reached.p, E * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+        HIPCHECK(hipStreamSynchronize(ctx->stream));
+    }
+    // one job per missing (C, X): C's first m vectors against X's range
+    std::vector<Job> jobs;
+    std::vector<uint32_t> seg_start, seg_vend, job_c, job_per;
+    std::vector<uint2> rows;
+    uint64_t total_edges = 0, pairs = 0;
+    if (per_max > 0) {
+        for (uint32_t c = 1; c <= G; ++c) {
+            const uint32_t nc = group_begin[c + 1] - group_begin[c];
+            for (uint32_t p = out_ptr[c]; p < out_ptr[c + 1]; ++p) {
+                if (reached[p])
+                    continue;
+                const uint32_t x = out_idx[p];
+                const uint32_t nx = group_begin[x + 1] - group_begin[x];
+                const uint32_t per = std::min(nx, per_max);
+                if (per == 0 || nc == 0)
+                    continue;
+                const uint32_t m = std::min<uint32_t>(nc, (num_cross + per - 1) / per);
+                Job jb{};
+                jb.q_begin = group_begin[c];
+                jb.q_count = m;
+                jb.seg_begin = (uint32_t)seg_start.size();
+                jb.seg_count = 1;
+                jb.n_cand = nx;
+                jb.n_split = 1;
+                jb.split_v = nx;
+                jb.out_row = (uint32_t)rows.size();
+                seg_start.push_back(group_begin[x]);
+                seg_vend.push_back(nx);
+                for (uint32_t j = 0; j < m; ++j)
+                    rows.push_back(make_uint2((uint32_t)jobs.size(), j));
+                jobs.push_back(jb);
+                job_c.push_back(c);
+                job_per.push_back(per);
+                total_edges += (uint64_t)m * per;
+                pairs += (uint64_t)m * nx;
+                if (rows.size() >= 0xFFFFFFFFull) {
+                    set_error("ung_hip_additional_edges: more than 2^32 query rows");
+                    return UNG_HIP_EINVAL;
+                }
+            }
+        }
+    }
+    *n_edges = total_edges;
+    if (total_edges > capacity || (total_edges > 0 && (!edge_from || !edge_to))) {
+        set_error("ung_hip_additional_edges: %llu edges need capacity (got %llu)", (unsigned long long)total_edges,
+                  (unsigned long long)capacity);
+        return UNG_HIP_EINVAL;
+    }
+    if (st) {
+        st->plan_ms += ms_since(t0);
+        st->rows += rows.size();
+        st->pairs += pairs;
+        st->work_items += jobs.size();
+    }
+    std::vector<uint32_t> ids;
+    std::vector<int32_t> size;
+    if (!rows.empty()) {
+        const uint64_t R = rows.size();
+        if ((rc = ctx->jobs.ensure(jobs.size())) || (rc = ctx->seg_start.ensure(seg_start.size())) ||
+            (rc = ctx->seg_vend.ensure(seg_vend.size())) || (rc = ctx->flagged.ensure(R)) ||
+            (rc = ctx->flag_count.ensure(2)) || (rc = ctx->a_ids.ensure(R * per_max)) || (rc = ctx->a_size.ensure(R)))
+            return rc;
+        const uint32_t nrows = (uint32_t)R;
+        HIPCHECK(hipMemcpyAsync(ctx->jobs.p, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->seg_start.p, seg_start.data(), seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->seg_vend.p, seg_vend.data(), seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->flagged.p, rows.data(), R * sizeof(uint2), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->flag_count.p, &nrows, sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipEventRecord(ctx->ev[0], ctx->stream));
+        FallbackParams F{};
+        F.X = ctx->X;
+        F.d = ctx->d;
+        F.k = per_max;
+        F.jobs = ctx->jobs.p;
+        F.seg_start = ctx->seg_start.p;
+        F.seg_vend = ctx->seg_vend.p;
+        F.flag_count = ctx->flag_count.p;
+        F.flagged = ctx->flagged.p;
+        F.out_ids = ctx->a_ids.p;
+        F.out_dist = nullptr;
+        F.out_size = ctx->a_size.p;
+        hipLaunchKernelGGL(ung_fallback_kernel, dim3(std::min<uint32_t>(nrows, 8192u)), dim3(64), 0, ctx->stream, F);
+        HIPCHECK(hipGetLastError());
+        HIPCHECK(hipEventRecord(ctx->ev[1], ctx->stream));
+        ids.resize(R * per_max);
+        size.resize(R);
+        HIPCHECK(hipMemcpyAsync(ids.data(), ctx->a_ids.p, ids.size() * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(size.data(), ctx->a_size.p, R * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+        HIPCHECK(hipStreamSynchronize(ctx->stream));
+        if (st) {
+            float ms = 0;
+            HIPCHECK(hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[1]));
+            st->fallback_ms += ms;
+            st->kernel_ms += ms;
+        }
+    }
+    // compact into per-group lists in the reference's append order
+    uint64_t n = 0;
+    size_t ji = 0;
+    edge_ptr[0] = edge_ptr[1] = 0;
+    for (uint32_t c = 1; c <= G; ++c) {
+        for (; ji < jobs.size() && job_c[ji] == c; ++ji) {
+            const Job &jb = jobs[ji];
+            for (uint32_t j = 0; j < jb.q_count; ++j) {
+                const uint32_t r = jb.out_row + j;
+                const uint32_t cnt = std::min<uint32_t>((uint32_t)size[r], job_per[ji]);
+                for (uint32_t t = 0; t < cnt; ++t) {
+                    edge_from[n] = jb.q_begin + j;
+                    edge_to[n] = ids[(size_t)r * per_max + t];
+                    ++n;
+                }
+            }
+        }
+        edge_ptr[c + 1] = (uint32_t)n;
+    }
+    if (n != total_edges) {
+        set_error("ung_hip_additional_edges: %llu edges produced, %llu expected", (unsigned long long)n,
+                  (unsigned long long)total_edges);
+        return UNG_HIP_EDEVICE;
+    }
+    if (st)
+        st->wall_ms += ms_since(t0);
+    return UNG_HIP_OK;
+}
+
 int download(ung_hip_ctx *ctx, ResultBufs &res, uint32_t *ids, float *dist, int32_t *size, ung_hip_stats *st)
 {
     if (!res.valid) {
@@ -1910,6 +2139,13 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     ctx->gjobs.release();
     ctx->gmitems.release();
     ctx->graph.release();
+    ctx->a_gb.release();
+    ctx->a_op.release();
+    ctx->a_oi.release();
+    ctx->a_pg.release();
+    ctx->a_reached.release();
+    ctx->a_ids.release();
+    ctx->a_size.release();
     for (auto &ev : ctx->ev)
         if (ev)
             (void)hipEventDestroy(ev);
@@ -1981,6 +2217,15 @@ int ung_hip_download_cross(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist,
         return UNG_HIP_EINVAL;
     }
     return download(ctx, ctx->cross, out_ids, out_dist, out_size, st);
+}
+
+int ung_hip_additional_edges(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
+                             const uint32_t *out_idx, uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
+                             uint32_t *edge_to, uint64_t capacity, uint64_t *n_edges, ung_hip_stats *st)
+{
+    clear_error();
+    return additional_device(ctx, G, group_begin, out_ptr, out_idx, num_cross, edge_ptr, edge_from, edge_to, capacity,
+                             n_edges, st);
 }
 
 int ung_hip_group_knn_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,

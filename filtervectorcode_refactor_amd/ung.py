@@ -112,6 +112,29 @@ class HipContext:
         check(self.lib.ung_hip_download_cross(self.h, ptr(ids), ptr(dist), ptr(size), C.byref(st)))
         return ids, dist, size, st.as_dict()
 
+    def additional_edges(self, group_begin, out_ptr, out_idx, num_cross: int):
+        """Additional edges (exact variant) from the resident cross-edge rows of the last
+        cross_topk(_device) call: (edge_ptr[G+2], edge_from, edge_to, stats); the edges of
+        group C are [edge_ptr[C], edge_ptr[C+1]).  stats["fallback_ms"] is the exact-scan
+        kernel time, stats["rows"] the query rows scanned."""
+        group_begin, out_ptr = u32(group_begin), u32(out_ptr)
+        out_idx = u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
+        G = group_begin.shape[0] - 2
+        edge_ptr = np.zeros(G + 2, np.uint32)
+        n = C.c_uint64(0)
+        cap = max(1024, int(group_begin[-1]) // 8)
+        while True:
+            ef = np.empty(cap, np.uint32)
+            et = np.empty(cap, np.uint32)
+            st = Stats()
+            rc = self.lib.ung_hip_additional_edges(self.h, G, ptr(group_begin), ptr(out_ptr), ptr(out_idx), num_cross,
+                                                   ptr(edge_ptr), ptr(ef), ptr(et), cap, C.byref(n), C.byref(st))
+            if rc == _lib.UNG_HIP_EINVAL and n.value > cap:
+                cap = int(n.value)
+                continue
+            check(rc)
+            return edge_ptr, ef[: n.value].copy(), et[: n.value].copy(), st.as_dict()
+
     def group_knn(self, grp_begin, grp_size, list_k: int):
         grp_begin, grp_size = u32(grp_begin), u32(grp_size)
         rows = int(grp_size.astype(np.uint64).sum())
@@ -342,6 +365,19 @@ class UngBuildStage:
         self.cross_flat_ids, self.cross_dists, self.cross_sizes = ids, dist, size
         self.cross_stats = st
         return ids, dist, size
+
+    def build_cross_edges_generate_additional(self):
+        """Additional edges, exact variant (build_cross_edges_generate_additional,
+        src/uni_nav_graph_cross_edges.cpp:442-596): per group C, the out-groups that no
+        cross edge of C's members reaches get num_cross/2 exact nearest targets from each of
+        C's first vectors until num_cross edges were added.  Needs the cross edges of
+        gpu_cross_groups_search_all_batched on the device.  Returns the per-group CSR
+        (edge_ptr[G+2], edge_from, edge_to) -- the reference's materialized lists."""
+        ptr_, ef, et, st = self.ctx.additional_edges(self.group_begin, self.out_ptr, self.out_idx,
+                                                     self.num_cross_edges)
+        self.additional_edges = (ptr_, ef, et)
+        self.additional_stats = st
+        return ptr_, ef, et
 
     def mid_groups(self):
         """Groups routed to the exact batch (partition_tagore_groups +

@@ -113,6 +113,26 @@ int ung_hip_cross_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **di
 int ung_hip_download_cross(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist,
                            int32_t *out_size, ung_hip_stats *st);
 
+/* Additional edges, exact variant.  Replaces
+ * UniNavGraph::build_cross_edges_generate_additional (src/uni_nav_graph_cross_edges.cpp:
+ * 442-596, UngAdditionalEdgesImpl::CpuExactScan branch :543-562; special blocks off):
+ * for every group C the out-groups X (LNG row order) that no cross edge of C's members
+ * reaches get edges from C's first vectors -- each vector the first num_cross/2 entries
+ * of an exact (distance, id) SearchQueue(num_cross) over X -- until at least num_cross
+ * edges were added for X or C has no more vectors.
+ * Uses the cross-edge rows left in HBM by the last ung_hip_cross_topk(_device) call (same
+ * G, group_begin, out_ptr, out_idx; num_cross <= that call's k; its first num_cross
+ * entries per row are read, as the reference reads its FlatId rows, :500-512).
+ * Output (host memory): edge_ptr[G+2] CSR over groups 1..G (the materialized per-group
+ * lists of the reference, edges of C in [edge_ptr[C], edge_ptr[C+1])), edge_from /
+ * edge_to global new ids, in the reference's append order.  capacity = entries of
+ * edge_from/edge_to; *n_edges receives the count; UNG_HIP_EINVAL (nothing written) when
+ * capacity is too small. */
+int ung_hip_additional_edges(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
+                             const uint32_t *out_ptr, const uint32_t *out_idx, uint32_t num_cross,
+                             uint32_t *edge_ptr, uint32_t *edge_from, uint32_t *edge_to,
+                             uint64_t capacity, uint64_t *n_edges, ung_hip_stats *st);
+
 /* Exact intra-group kNN for a batch of groups.  Replaces the exact list computed by
  * batched_exact_knn_graph_kernel (src/tagore_graph_builder.cu:650-728, host driver
  * build_fast_exact_cuda_batch :1058-1429) with the semantics of the CPU builder

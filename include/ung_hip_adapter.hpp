@@ -119,6 +119,44 @@ class Backend {
                 sink((uint32_t)p, ids_[p * k_ + j], dists_[p * k_ + j]);
     }
 
+    // UniNavGraph::build_cross_edges_generate_additional, exact variant
+    // (src/uni_nav_graph_cross_edges.cpp:442-596) after cross_groups_search_all_batched:
+    // materialized[C] = the (from, to) pairs appended for group C, in the reference's
+    // order (materialized has G+1 entries; entry 0 is unused).
+    void cross_edges_generate_additional(const GroupRanges &group_id_to_range, const GroupRows &out_neighbors,
+                                         uint32_t num_cross_edges,
+                                         std::vector<std::vector<std::pair<uint32_t, uint32_t>>> &materialized)
+    {
+        const uint32_t G = (uint32_t)group_id_to_range.size() - 1;
+        std::vector<uint32_t> group_begin(G + 2, 0), out_ptr(G + 2, 0), out_idx;
+        for (uint32_t g = 1; g <= G; ++g)
+            group_begin[g + 1] = group_id_to_range[g].second;
+        for (uint32_t c = 1; c <= G; ++c) {
+            if (c < out_neighbors.size())
+                out_idx.insert(out_idx.end(), out_neighbors[c].begin(), out_neighbors[c].end());
+            out_ptr[c + 1] = (uint32_t)out_idx.size();
+        }
+        std::vector<uint32_t> edge_ptr(G + 2, 0), from, to;
+        uint64_t n = 0, cap = group_begin[G + 1] / 8 + 1024;
+        for (;;) {
+            from.resize(cap);
+            to.resize(cap);
+            const int rc = ung_hip_additional_edges(ctx_, G, group_begin.data(), out_ptr.data(),
+                                                    out_idx.empty() ? nullptr : out_idx.data(), num_cross_edges,
+                                                    edge_ptr.data(), from.data(), to.data(), cap, &n, &last_);
+            if (rc == UNG_HIP_EINVAL && n > cap) {
+                cap = n;
+                continue;
+            }
+            throw_if(rc, "cross_edges_generate_additional");
+            break;
+        }
+        materialized.assign(G + 1, {});
+        for (uint32_t c = 1; c <= G; ++c)
+            for (uint32_t e = edge_ptr[c]; e < edge_ptr[c + 1]; ++e)
+                materialized[c].emplace_back(from[e], to[e]);
+    }
+
     // build_fast_exact_cuda_batch (src/tagore_graph_builder.cu:1058-1429) for groups
     // that are contiguous id ranges of the resident base set: exact top lists +
     // anchor-packed rows [deg, ids...] with stride final_degree+1.

@@ -33,6 +33,32 @@ def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+_ADDL_ARGS = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, _u32p, _u32p, _u32p, _u32p, C.c_uint32,
+              C.c_uint32, _u32p, _u32p, _u32p, C.c_int64, C.POINTER(C.c_int64)]
+
+
+def _additional_edges(fn, X, group_begin, out_ptr, out_idx, cross_ids, num_cross):
+    """Shared driver of the two additional-edge restatements: returns
+    (edge_ptr[G+2], edge_from, edge_to)."""
+    X = _f32(X)
+    N, d = X.shape
+    G = group_begin.shape[0] - 2
+    cross_ids = _u32(cross_ids)
+    stride = cross_ids.shape[1] if cross_ids.ndim == 2 else 1
+    out_idx = _u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
+    ptr = np.zeros(G + 2, np.uint32)
+    need = C.c_int64(0)
+    cap = 1 << 16
+    while True:
+        ef = np.zeros(cap, np.uint32)
+        et = np.zeros(cap, np.uint32)
+        n = fn(X, N, d, G, _u32(group_begin), _u32(out_ptr), out_idx, cross_ids.reshape(-1), stride,
+               num_cross, ptr, ef, et, cap, C.byref(need))
+        if n >= 0:
+            return ptr, ef[:n].copy(), et[:n].copy()
+        cap = int(need.value)
+
+
 class Oracle:
     """Plain-C restatement of the reference CPU semantics."""
 
@@ -61,6 +87,8 @@ class Oracle:
         L.ungo_intra_exact.restype = None
         L.ungo_intra_exact.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                        _u32p, _f32p, C.c_int]
+        L.ungo_additional_edges.restype = C.c_int64
+        L.ungo_additional_edges.argtypes = _ADDL_ARGS
         L.ungo_pack_anchor_row.restype = None
         L.ungo_pack_anchor_row.argtypes = [_u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                            C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
@@ -143,6 +171,10 @@ class Oracle:
         self.lib.ungo_intra_exact(X, X.shape[1], begin, n, K, ids, dists, nthreads)
         return ids, dists
 
+    def additional_edges(self, X, group_begin, out_ptr, out_idx, cross_ids, num_cross):
+        return _additional_edges(self.lib.ungo_additional_edges, X, group_begin, out_ptr, out_idx,
+                                 cross_ids, num_cross)
+
     def pack_anchor_row(self, top_idx, cand_degree, n, local_src, final_degree, head_keep,
                         anchor_tail=1, anchor_slots=0, bidir_anchor=0, graph_stride=None):
         if graph_stride is None:
@@ -174,6 +206,8 @@ class RefOracle:
         L.ungref_intra_exact.restype = None
         L.ungref_intra_exact.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                          _u32p, _f32p, C.c_int]
+        L.ungref_additional_edges.restype = C.c_int64
+        L.ungref_additional_edges.argtypes = _ADDL_ARGS
         self.lib = L
 
     def l2(self, a, b) -> float:
@@ -217,6 +251,10 @@ class RefOracle:
         dists = np.zeros((n, K), np.float32)
         self.lib.ungref_intra_exact(X, X.shape[1], begin, n, K, ids, dists, nthreads)
         return ids, dists
+
+    def additional_edges(self, X, group_begin, out_ptr, out_idx, cross_ids, num_cross):
+        return _additional_edges(self.lib.ungref_additional_edges, X, group_begin, out_ptr, out_idx,
+                                 cross_ids, num_cross)
 
 
 def ref_available() -> bool:

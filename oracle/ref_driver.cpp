@@ -13,6 +13,8 @@
 //                          (src/uni_nav_graph_cross_edges.cpp:154-220, :32-57)
 //   ungref_intra_exact  -> build_exact_topk_graph_for_points
 //                          (src/uni_nav_graph_special_blocks.cpp:70-111)
+//   ungref_additional_edges -> build_cross_edges_generate_additional, exact branch
+//                          (src/uni_nav_graph_cross_edges.cpp:442-596)
 // (their host file needs Boost and cannot be compiled here).
 #include <algorithm>
 #include <cmath>
@@ -167,6 +169,60 @@ void ungref_intra_exact(const float *X, uint32_t dim, uint32_t begin, uint32_t n
             ds[j] = cand[j].first;
         }
     }
+}
+
+// Additional edges, CPU exact variant (UniNavGraph::build_cross_edges_generate_additional,
+// src/uni_nav_graph_cross_edges.cpp:442-596, CpuExactScan branch :543-562, special
+// blocks off), with the reference's own SearchQueue and distance.  Same contract as
+// ungo_additional_edges in oracle/ung_oracle.h.
+int64_t ungref_additional_edges(const float *X, uint32_t N, uint32_t dim, uint32_t G,
+                                const uint32_t *group_begin, const uint32_t *out_ptr,
+                                const uint32_t *out_idx, const uint32_t *cross_ids, uint32_t stride,
+                                uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
+                                uint32_t *edge_to, int64_t cap, int64_t *needed)
+{
+    const FloatL2DistanceHandler h;
+    std::vector<uint32_t> pg(N);
+    for (uint32_t g = 1; g <= G; ++g)
+        for (uint32_t i = group_begin[g]; i < group_begin[g + 1]; ++i)
+            pg[i] = g;
+    std::vector<uint32_t> connected_epoch((size_t)G + 1, 0);
+    const uint32_t use = std::min(num_cross, stride);
+    int64_t n = 0;
+    edge_ptr[0] = edge_ptr[1] = 0;
+    for (uint32_t c = 1; c <= G; ++c) {
+        for (uint32_t i = group_begin[c]; i < group_begin[c + 1]; ++i)
+            for (uint32_t t = 0; t < use; ++t) {
+                const uint32_t nb = cross_ids[(size_t)i * stride + t];
+                if (nb != UINT32_MAX)
+                    connected_epoch[pg[nb]] = c;
+            }
+        for (uint32_t p = out_ptr[c]; p < out_ptr[c + 1]; ++p) {
+            const uint32_t x = out_idx[p];
+            if (connected_epoch[x] == c)
+                continue;
+            uint32_t cnt = 0;
+            for (uint32_t v = group_begin[c]; v < group_begin[c + 1] && cnt < num_cross; ++v) {
+                SearchQueue local_topk;
+                local_topk.reserve((int32_t)num_cross);
+                const char *qv = reinterpret_cast<const char *>(X + (size_t)v * dim);
+                for (uint32_t t = group_begin[x]; t < group_begin[x + 1]; ++t)
+                    local_topk.insert(t, h.compute(qv, reinterpret_cast<const char *>(X + (size_t)t * dim), dim));
+                for (int k = 0; k < local_topk.size() && k < (int)(num_cross / 2); ++k) {
+                    if (n < cap) {
+                        edge_from[n] = v;
+                        edge_to[n] = local_topk[k].id;
+                    }
+                    ++n;
+                    ++cnt;
+                }
+            }
+        }
+        edge_ptr[c + 1] = (uint32_t)n;
+    }
+    if (needed)
+        *needed = n;
+    return n <= cap ? n : -1;
 }
 
 } // extern "C"

@@ -370,6 +370,63 @@ void ungo_cross_exact_points(const float *X, uint32_t N, uint32_t dim, uint32_t 
     }
 }
 
+/* ---- additional edges: uni_nav_graph_cross_edges.cpp:442-596 (exact branch :543-562) ---- */
+
+int64_t ungo_additional_edges(const float *X, uint32_t N, uint32_t dim, uint32_t G,
+                              const uint32_t *group_begin, const uint32_t *out_ptr,
+                              const uint32_t *out_idx, const uint32_t *cross_ids, uint32_t stride,
+                              uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
+                              uint32_t *edge_to, int64_t cap, int64_t *needed)
+{
+    uint32_t *pg = (uint32_t *)malloc(sizeof(uint32_t) * (N ? N : 1));
+    uint32_t *mark = (uint32_t *)calloc((size_t)G + 1, sizeof(uint32_t));
+    uint32_t *qi = (uint32_t *)malloc(sizeof(uint32_t) * (num_cross + 1));
+    float *qd = (float *)malloc(sizeof(float) * (num_cross + 1));
+    for (uint32_t g = 1; g <= G; ++g)
+        for (uint32_t i = group_begin[g]; i < group_begin[g + 1]; ++i)
+            pg[i] = g;
+    const uint32_t use = num_cross < stride ? num_cross : stride;
+    int64_t n = 0;
+    edge_ptr[0] = edge_ptr[1] = 0;
+    for (uint32_t c = 1; c <= G; ++c) {
+        const uint32_t s = group_begin[c], e = group_begin[c + 1];
+        for (uint32_t i = s; i < e; ++i)
+            for (uint32_t t = 0; t < use; ++t) {
+                const uint32_t nb = cross_ids[(size_t)i * stride + t];
+                if (nb != UINT32_MAX)
+                    mark[pg[nb]] = c; /* epoch = C */
+            }
+        for (uint32_t p = out_ptr[c]; p < out_ptr[c + 1]; ++p) {
+            const uint32_t x = out_idx[p];
+            if (mark[x] == c)
+                continue;
+            uint32_t cnt = 0;
+            for (uint32_t v = s; v < e && cnt < num_cross; ++v) {
+                int32_t size = 0;
+                const float *qv = X + (size_t)v * dim;
+                for (uint32_t t = group_begin[x]; t < group_begin[x + 1]; ++t)
+                    ungo_queue_insert(qi, qd, &size, (int32_t)num_cross, t, ungo_l2(qv, X + (size_t)t * dim, dim));
+                for (int32_t j = 0; j < size && j < (int32_t)(num_cross / 2); ++j) {
+                    if (n < cap) {
+                        edge_from[n] = v;
+                        edge_to[n] = qi[j];
+                    }
+                    ++n;
+                    ++cnt;
+                }
+            }
+        }
+        edge_ptr[c + 1] = (uint32_t)n;
+    }
+    free(pg);
+    free(mark);
+    free(qi);
+    free(qd);
+    if (needed)
+        *needed = n;
+    return n <= cap ? n : -1;
+}
+
 /* ---- intra-group exact top-K: uni_nav_graph_special_blocks.cpp:70-111 ---- */
 
 void ungo_intra_exact(const float *X, uint32_t dim, uint32_t begin, uint32_t n, uint32_t K,

@@ -86,6 +86,22 @@ void ungo_cross_exact_points(const float *X, uint32_t N, uint32_t dim, uint32_t 
                              uint32_t *out_ids, float *out_dists, int32_t *out_size,
                              int nthreads);
 
+/* Additional edges, CPU exact variant, restating
+ * UniNavGraph::build_cross_edges_generate_additional (src/uni_nav_graph_cross_edges.cpp:
+ * 442-596, CpuExactScan branch :543-562; special blocks off):
+ *   for C = 1..G: the groups reached by the first num_cross entries of the cross-edge
+ *   rows of C's members (cross_ids[N x stride], UINT32_MAX = none) are connected; for
+ *   every X of out(C) (row order) that is not, vectors v = s_C, s_C+1, ... while fewer
+ *   than num_cross edges were appended for this X get the first num_cross/2 entries of an
+ *   exact SearchQueue(num_cross) over X's range (ids ascending).
+ * out: edge_ptr[G+2] CSR over groups 1..G, edge_from/edge_to (global new ids) in that
+ * order.  Returns the edge count; -1 when cap is too small (*needed = the count). */
+int64_t ungo_additional_edges(const float *X, uint32_t N, uint32_t dim, uint32_t G,
+                              const uint32_t *group_begin, const uint32_t *out_ptr,
+                              const uint32_t *out_idx, const uint32_t *cross_ids, uint32_t stride,
+                              uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
+                              uint32_t *edge_to, int64_t cap, int64_t *needed);
+
 /* Exact intra-group top-K, restating build_exact_topk_graph_for_points
  * (src/uni_nav_graph_special_blocks.cpp:70-111): for every point i of the
  * group [begin, begin+n) the first min(K, n-1) local ids j != i ordered by

@@ -2,7 +2,8 @@
 """Writes the golden fixtures of tests/golden/ from the reference's OWN compiled
 code: oracle/_ref/libungref.so = UNG/codes/src/distance.cpp + search_queue.cpp
 built from /root/reference by oracle/Makefile, driven by oracle/ref_driver.cpp
-(restating build_cross_edges_generate_cpu_exact_scan and
+(restating build_cross_edges_generate_cpu_exact_scan,
+build_cross_edges_generate_additional (exact branch) and
 build_exact_topk_graph_for_points around those objects).
 
 Inputs come from the product's seeded generator (cfg1 and a d=384 normalised
@@ -40,6 +41,8 @@ def make(cfg, name, k_cross=6, k_intra=32, intra_row_stride=1):
     st = F.UngBuildStage()
     st.prepare_inputs(X, lp, li)
     ids, dists, size = ref.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, k_cross)
+    addl_ptr, addl_from, addl_to = ref.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx,
+                                                        ids, k_cross)
     gids = st.mid_groups()
     rows_i, rows_d, grp_of_row, local_row = [], [], [], []
     for g in gids:
@@ -57,6 +60,7 @@ def make(cfg, name, k_cross=6, k_intra=32, intra_row_stride=1):
         group_begin=st.group_begin, out_ptr=st.out_ptr, out_idx=st.out_idx,
         cross_ids=ids, cross_dists=dists, cross_size=size,
         cross_sha256=np.array(sha(ids, dists, size)),
+        addl_ptr=addl_ptr, addl_from=addl_from, addl_to=addl_to,
         intra_groups=gids, intra_k=np.array(k_intra),
         intra_sha256=np.array(sha(intra_ids, intra_d)),
         intra_rows=keep.astype(np.uint32),

@@ -125,4 +125,11 @@ def test_cfg2_full_size(oracle):
         o_i, o_d = chk.intra_exact(st.base, b, n, 32)
         r0 = row_of[int(g)]
         _assert_rows_equal(kids[r0: r0 + n], kdist[r0: r0 + n], None, o_i, o_d, None, f"cfg2 full intra {g}")
+    # additional edges from the same (resident) cross rows, against the oracle fed those rows
+    ctx.cross_topk_device(st.group_begin, st.out_ptr, st.out_idx, 6)
+    got = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, 6)
+    print(f"cfg2 full: {got[1].size} additional edges, stats {got[3]}", flush=True)
+    want = oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, ids, 6)
+    for a, b in zip(got[:3], want):
+        assert np.array_equal(a, b)
     st.close()

@@ -198,3 +198,60 @@ def test_cfg2_scaled_parity(ctx, oracle):
         o_i, o_d = oracle.intra_exact(st.base, int(b), int(n), 32)
         _assert_rows_equal(ids[row: row + n], dist[row: row + n], None, o_i, o_d, None, f"cfg2@60k intra {b}")
         row += n
+
+
+# ---------------------------------------------------------------- additional edges
+def _assert_edges_equal(got, want, what):
+    for name, a, b in zip(("edge_ptr", "edge_from", "edge_to"), got[:3], want):
+        assert np.array_equal(a, b), f"{what}: {name} differs"
+
+
+def test_additional_edges_cfg1(ctx, cfg1_stage, oracle):
+    st = cfg1_stage
+    ctx.prepare_vectors(st.base)
+    ids, _, _, _ = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+    got = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, 6)
+    _say(f"additional cfg1: {got[1].size} edges, stats {got[3]}")
+    want = oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, ids, 6)
+    assert got[1].size > 0
+    _assert_edges_equal(got, want, "cfg1 additional")
+
+
+@pytest.mark.parametrize("k", [6, 7, 2, 1])
+def test_additional_edges_closed_form_problem(ctx, oracle, k):
+    from test_oracle import _addl_problem
+    X, gb, op, oi = _addl_problem(np.random.default_rng(3))
+    ctx.prepare_vectors(X)
+    ids, _, _, _ = ctx.cross_topk(gb, op, oi, k)
+    got = ctx.additional_edges(gb, op, oi, k)
+    want = oracle.additional_edges(X, gb, op, oi, ids, k)
+    _assert_edges_equal(got, want, f"closed-form problem k={k}")
+    assert (got[1].size == 0) == (k < 2)
+
+
+def test_additional_edges_errors(ctx):
+    X = np.zeros((10, 8), np.float32)
+    ctx.prepare_vectors(X)
+    gb = np.array([0, 0, 5, 10], np.uint32)
+    op = np.array([0, 0, 1, 1], np.uint32)
+    oi = np.array([2], np.uint32)
+    with pytest.raises(F.UngHipError) as e:
+        ctx.additional_edges(gb, op, oi, 6)  # no cross edges computed for these vectors
+    assert e.value.code == -3
+    ctx.cross_topk(gb, op, oi, 4)
+    with pytest.raises(F.UngHipError) as e:
+        ctx.additional_edges(gb, op, oi, 5)  # more than the k of the cross call
+    assert e.value.code == -1
+
+
+def test_additional_edges_cfg2_scaled(ctx, oracle):
+    cfg = D.scaled(D.CONFIGS["cfg2"], 60_000)
+    X, lp, li = D.generate(cfg)
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    ctx.prepare_vectors(st.base)
+    ids, _, _, _ = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+    got = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, 6)
+    want = oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, ids, 6)
+    _say(f"additional cfg2@60k: {got[1].size} edges")
+    _assert_edges_equal(got, want, "cfg2@60k additional")
