@@ -81,6 +81,9 @@ SIGNATURES = {
     "ung_group_label_sets": (_int, [_u64, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _u64]),
     "ung_lng_build": (_int, [_u32, _vp, _vp, _vp, _vp, _u64, C.POINTER(_u64), _int]),
     "ung_reorder_rows": (_int, [_vp, _u64, _u32, _vp, _vp, _int]),
+    "ung_assemble_graph_csr": (_int, [_u64, _u32, _vp, _vp, _vp, _int, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp,
+                                      _u64, C.POINTER(_u64), _int]),
+    "ung_graph_save_text": (_int, [C.c_char_p, _u64, _vp, _vp, _int]),
     "ung_count_pairs": (_int, [_u32, _vp, _vp, _vp, _u32, _u32, C.POINTER(_u64), C.POINTER(_u64)]),
     "ung_synth_vectors": (_int, [_u64, _u32, _u32, C.c_float, C.c_float, _int, _u64, _u64, _vp, _int]),
     "ung_synth_labels": (_int, [_u64, _int, _u32, _u32, _u32, _dbl, _u64, _vp, _vp, _int]),

@@ -479,4 +479,148 @@ extern "C" int ung_count_pairs(uint32_t G, const uint32_t *group_begin, const ui
     return UNG_HIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Output boundary: the final adjacency as CSR and the Graph::save text format
+// ---------------------------------------------------------------------------
+extern "C" int ung_assemble_graph_csr(uint64_t N, uint32_t G, const uint32_t *group_begin, const uint64_t *intra_ptr,
+                                      const uint32_t *intra_idx, int intra_global, const uint32_t *cross_ids,
+                                      uint32_t cross_stride, uint32_t num_cross, const uint32_t *add_ptr,
+                                      const uint32_t *add_from, const uint32_t *add_to, uint64_t *row_ptr,
+                                      uint32_t *col_idx, uint64_t capacity, uint64_t *n_entries, int nthreads)
+{
+    clear_error();
+    if (!group_begin || !row_ptr || !n_entries || (intra_ptr && !intra_idx && intra_ptr[N] > 0) ||
+        (cross_ids && num_cross > cross_stride) || (add_ptr && (!add_from || !add_to) && add_ptr[G + 1] > 0)) {
+        set_error("ung_assemble_graph_csr: null or inconsistent argument");
+        return UNG_HIP_EINVAL;
+    }
+    if ((uint64_t)group_begin[G + 1] != N) {
+        set_error("ung_assemble_graph_csr: group_begin[G+1]=%u != N=%llu", group_begin[G + 1], (unsigned long long)N);
+        return UNG_HIP_EINVAL;
+    }
+    const uint32_t use = cross_ids ? num_cross : 0u;
+    // point -> first id of its group (add_offset_for_uni_nav_graph) and per-point counts
+    std::vector<uint32_t> base(N);
+    std::vector<uint64_t> cnt(N + 1, 0);
+    for (uint32_t g = 1; g <= G; ++g) {
+        if (group_begin[g + 1] < group_begin[g]) {
+            set_error("ung_assemble_graph_csr: group_begin not monotone at group %u", g);
+            return UNG_HIP_EINVAL;
+        }
+        for (uint64_t i = group_begin[g]; i < group_begin[g + 1]; ++i)
+            base[i] = group_begin[g];
+    }
+    parallel_for((int64_t)N, nthreads, 65536, [&](int64_t b, int64_t e) {
+        for (int64_t i = b; i < e; ++i) {
+            uint64_t c = intra_ptr ? intra_ptr[i + 1] - intra_ptr[i] : 0;
+            for (uint32_t t = 0; t < use; ++t)
+                c += cross_ids[(uint64_t)i * cross_stride + t] != 0xFFFFFFFFu;
+            cnt[i + 1] = c;
+        }
+    });
+    if (add_ptr)
+        for (uint32_t g = 1; g <= G; ++g)
+            for (uint64_t e = add_ptr[g]; e < add_ptr[g + 1]; ++e) {
+                // a group's list holds edges from its own points only (one writer per row)
+                if (add_from[e] < group_begin[g] || add_from[e] >= group_begin[g + 1]) {
+                    set_error("ung_assemble_graph_csr: additional edge %llu of group %u starts at %u, outside the group",
+                              (unsigned long long)e, g, add_from[e]);
+                    return UNG_HIP_EINVAL;
+                }
+                ++cnt[add_from[e] + 1];
+            }
+    for (uint64_t i = 0; i < N; ++i)
+        cnt[i + 1] += cnt[i];
+    *n_entries = cnt[N];
+    if (cnt[N] > capacity || (cnt[N] > 0 && !col_idx)) {
+        set_error("ung_assemble_graph_csr: %llu entries need capacity (got %llu)", (unsigned long long)cnt[N],
+                  (unsigned long long)capacity);
+        return UNG_HIP_EINVAL;
+    }
+    std::memcpy(row_ptr, cnt.data(), (N + 1) * sizeof(uint64_t));
+    // intra (+ group offset) then cross edges; cursors left at the end of each row's cross part
+    std::vector<uint64_t> cur(N);
+    parallel_for((int64_t)N, nthreads, 65536, [&](int64_t b, int64_t e) {
+        for (int64_t i = b; i < e; ++i) {
+            uint64_t w = row_ptr[i];
+            if (intra_ptr)
+                for (uint64_t p = intra_ptr[i]; p < intra_ptr[i + 1]; ++p)
+                    col_idx[w++] = intra_idx[p] + (intra_global ? 0u : base[i]);
+            for (uint32_t t = 0; t < use; ++t) {
+                const uint32_t nb = cross_ids[(uint64_t)i * cross_stride + t];
+                if (nb != 0xFFFFFFFFu)
+                    col_idx[w++] = nb;
+            }
+            cur[i] = w;
+        }
+    });
+    // additional edges, group list by group list (a group's lists only hold its own points)
+    if (add_ptr)
+        parallel_for((int64_t)G, nthreads, 256, [&](int64_t b, int64_t e) {
+            for (int64_t g = b + 1; g <= e; ++g)
+                for (uint64_t p = add_ptr[g]; p < add_ptr[g + 1]; ++p)
+                    col_idx[cur[add_from[p]]++] = add_to[p];
+        });
+    return UNG_HIP_OK;
+}
+
+extern "C" int ung_graph_save_text(const char *path, uint64_t N, const uint64_t *row_ptr, const uint32_t *col_idx,
+                                   int nthreads)
+{
+    clear_error();
+    if (!path || !row_ptr || (row_ptr[N] > 0 && !col_idx)) {
+        set_error("ung_graph_save_text: null argument");
+        return UNG_HIP_EINVAL;
+    }
+    FILE *f = std::fopen(path, "wb");
+    if (!f) {
+        set_error("ung_graph_save_text: cannot open %s", path);
+        return UNG_HIP_EINVAL;
+    }
+    // format blocks of points in parallel, write them in order: "i n1 n2 ... \n"
+    const int64_t block = 1 << 16;
+    const int64_t nblocks = ((int64_t)N + block - 1) / block;
+    const int wave = std::max(1, resolve_threads(nthreads)) * 2;
+    std::vector<std::string> text;
+    auto put = [](std::string &s, uint64_t v) {
+        char tmp[24];
+        int n = 0;
+        do {
+            tmp[n++] = (char)('0' + v % 10);
+            v /= 10;
+        } while (v);
+        while (n)
+            s.push_back(tmp[--n]);
+        s.push_back(' ');
+    };
+    bool ok = true;
+    for (int64_t b0 = 0; b0 < nblocks && ok; b0 += wave) {
+        const int64_t nb = std::min<int64_t>(wave, nblocks - b0);
+        text.assign((size_t)nb, std::string());
+        parallel_for(nb, nthreads, 1, [&](int64_t b, int64_t e) {
+            for (int64_t j = b; j < e; ++j) {
+                std::string &s = text[(size_t)j];
+                const uint64_t lo = (uint64_t)(b0 + j) * block, hi = std::min<uint64_t>(N, lo + block);
+                s.reserve((size_t)(hi - lo) * 16 + (size_t)(row_ptr[hi] - row_ptr[lo]) * 8);
+                for (uint64_t i = lo; i < hi; ++i) {
+                    put(s, i);
+                    for (uint64_t p = row_ptr[i]; p < row_ptr[i + 1]; ++p)
+                        put(s, col_idx[p]);
+                    s.push_back('\n');
+                }
+            }
+        });
+        for (const std::string &s : text)
+            if (std::fwrite(s.data(), 1, s.size(), f) != s.size()) {
+                ok = false;
+                break;
+            }
+    }
+    if (std::fclose(f) != 0 || !ok) {
+        set_error("ung_graph_save_text: write to %s failed", path);
+        return UNG_HIP_EINVAL;
+    }
+    return UNG_HIP_OK;
+}
+
 extern "C" const char *ung_hip_last_error(void) { return ung::g_last_error.c_str(); }

@@ -13,8 +13,11 @@ mid-group kNN stage (paths under UNG/codes/ of panjd123/FilterVectorCode_refacto
   build_fast_exact_batch            src/tagore_graph_builder.cu:1058-1429 (exact-anchor
                                     batch; exact lists as build_exact_topk_graph_for_points,
                                     src/uni_nav_graph_special_blocks.cpp:70-111)
+  build_cross_edges_generate_additional src/uni_nav_graph_cross_edges.cpp:442-596 (exact)
   merge_cross_edges_to_graph        src/ung_cross_edge_output_writer.cpp:68-95
   add_offset_for_uni_nav_graph      src/uni_nav_graph.cpp:285-297
+  build_csr_adjacency / Graph::save src/ung_cross_edge_output_writer.cpp:44-66,
+                                    include/graph.h:207-216
 
 Every device computation goes through libung_hip.so; failures raise
 ``RuntimeError`` (``UngHipError``), as the reference's GPU route throws
@@ -260,6 +263,46 @@ def count_pairs(group_begin, out_ptr, out_idx, intra_lo=128, intra_hi=4096):
     return pc.value, pi.value
 
 
+def assemble_graph_csr(N, group_begin, intra_ptr=None, intra_idx=None, intra_global=False, cross_ids=None,
+                       num_cross=None, add_ptr=None, add_from=None, add_to=None, nthreads: int = 0):
+    """Final adjacency as CSR (row_ptr[N+1] uint64, col_idx uint32): per point its intra
+    edges (group-local ids + the group's first id unless intra_global), the first
+    num_cross entries of its FlatId cross row, then its additional edges -- the
+    NeighborList the reference builds with add_offset_for_uni_nav_graph and the
+    cross/additional merges (src/uni_nav_graph.cpp:285-297,
+    src/uni_nav_graph_cross_edges.cpp:849-868)."""
+    lib = _lib.load()
+    group_begin = u32(group_begin)
+    G = group_begin.shape[0] - 2
+    ip = None if intra_ptr is None else np.ascontiguousarray(intra_ptr, np.uint64)
+    ii = None if intra_idx is None else (u32(intra_idx) if len(intra_idx) else np.zeros(1, np.uint32))
+    cr = None if cross_ids is None else u32(cross_ids)
+    stride = 0 if cr is None else (cr.shape[1] if cr.ndim == 2 else 1)
+    nc = stride if num_cross is None else int(num_cross)
+    ap = None if add_ptr is None else u32(add_ptr)
+    af = None if add_from is None else (u32(add_from) if len(add_from) else np.zeros(1, np.uint32))
+    at = None if add_to is None else (u32(add_to) if len(add_to) else np.zeros(1, np.uint32))
+    row_ptr = np.zeros(N + 1, np.uint64)
+    n = C.c_uint64(0)
+    rc = lib.ung_assemble_graph_csr(N, G, ptr(group_begin), ptr(ip), ptr(ii), int(intra_global), ptr(cr), stride, nc,
+                                    ptr(ap), ptr(af), ptr(at), ptr(row_ptr), None, 0, C.byref(n), nthreads)
+    if rc != _lib.UNG_HIP_EINVAL or n.value == 0:
+        check(rc)
+    col = np.empty(max(int(n.value), 1), np.uint32)
+    check(lib.ung_assemble_graph_csr(N, G, ptr(group_begin), ptr(ip), ptr(ii), int(intra_global), ptr(cr), stride,
+                                     nc, ptr(ap), ptr(af), ptr(at), ptr(row_ptr), ptr(col), col.shape[0],
+                                     C.byref(n), nthreads))
+    return row_ptr, col[: n.value]
+
+
+def graph_save_text(path, row_ptr, col_idx, nthreads: int = 0):
+    """Graph::save text format (include/graph.h:207-216): "i n1 n2 ... \\n" per point."""
+    lib = _lib.load()
+    row_ptr = np.ascontiguousarray(row_ptr, np.uint64)
+    col = u32(col_idx) if len(col_idx) else np.zeros(1, np.uint32)
+    check(lib.ung_graph_save_text(str(path).encode(), row_ptr.shape[0] - 1, ptr(row_ptr), ptr(col), nthreads))
+
+
 # ---------------------------------------------------------------------------
 # the stage object
 # ---------------------------------------------------------------------------
@@ -378,6 +421,23 @@ class UngBuildStage:
         self.additional_edges = (ptr_, ef, et)
         self.additional_stats = st
         return ptr_, ef, et
+
+    def build_csr_adjacency(self, intra_ptr=None, intra_idx=None, intra_global=False):
+        """The final graph as CSR (row_ptr[N+1], col_idx): intra edges (the group graphs'
+        local lists as CSR over points, offset by add_offset_for_uni_nav_graph unless
+        intra_global), the cross edges of gpu_cross_groups_search_all_batched, then the
+        additional edges of build_cross_edges_generate_additional when they were built."""
+        N = int(self.group_begin[-1])
+        add = getattr(self, "additional_edges", None)
+        cross = getattr(self, "cross_flat_ids", None)
+        self.graph_csr = assemble_graph_csr(N, self.group_begin, intra_ptr, intra_idx, intra_global, cross,
+                                            self.num_cross_edges if cross is not None else None,
+                                            *(add if add is not None else (None, None, None)))
+        return self.graph_csr
+
+    def save_graph(self, path):
+        """Graph::save of the assembled graph (include/graph.h:207-216)."""
+        graph_save_text(path, *self.graph_csr)
 
     def mid_groups(self):
         """Groups routed to the exact batch (partition_tagore_groups +

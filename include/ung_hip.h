@@ -181,6 +181,33 @@ int ung_hip_synchronize(ung_hip_ctx *ctx);
 int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err);
 
 /* ---------------------------------------------------------------------------
+ * Output boundary (CPU, multi-threaded C++).
+ * ------------------------------------------------------------------------- */
+
+/* The final adjacency as CSR: replaces the per-point NeighborList fill of
+ * add_offset_for_uni_nav_graph (src/uni_nav_graph.cpp:285-297),
+ * merge_cross_edges_to_graph + merge_additional_edges_to_graph
+ * (src/uni_nav_graph_cross_edges.cpp:849-868) and the writer's build_csr_adjacency
+ * (src/ung_cross_edge_output_writer.cpp:44-66, :104-147).  Row i = the intra-group
+ * edges of i (intra_ptr[N+1] / intra_idx, group-local ids plus the group's first id
+ * unless intra_global), then the first num_cross entries of its FlatId cross row
+ * (cross_ids [N x cross_stride], UINT32_MAX skipped; cross_ids may be NULL), then its
+ * additional edges in list order (add_ptr[G+2] CSR over groups as written by
+ * ung_hip_additional_edges; each group's list holds edges from its own points; may be
+ * NULL).  Output: row_ptr[N+1], col_idx (capacity entries); *n_entries = entries needed;
+ * UNG_HIP_EINVAL when capacity is too small. */
+int ung_assemble_graph_csr(uint64_t N, uint32_t G, const uint32_t *group_begin, const uint64_t *intra_ptr,
+                           const uint32_t *intra_idx, int intra_global, const uint32_t *cross_ids,
+                           uint32_t cross_stride, uint32_t num_cross, const uint32_t *add_ptr,
+                           const uint32_t *add_from, const uint32_t *add_to, uint64_t *row_ptr,
+                           uint32_t *col_idx, uint64_t capacity, uint64_t *n_entries, int nthreads);
+
+/* Graph::save text format (include/graph.h:207-216): one line per point,
+ * "i n1 n2 ... \n" with a space after every number, rows from a CSR. */
+int ung_graph_save_text(const char *path, uint64_t N, const uint64_t *row_ptr, const uint32_t *col_idx,
+                        int nthreads);
+
+/* ---------------------------------------------------------------------------
  * Host-side inputs of the path (CPU, multi-threaded C++).
  * ------------------------------------------------------------------------- */
 

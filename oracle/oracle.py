@@ -59,6 +59,39 @@ def _additional_edges(fn, X, group_begin, out_ptr, out_idx, cross_ids, num_cross
         cap = int(need.value)
 
 
+_ASM_ARGS = [C.c_uint64, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_uint32,
+             C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64]
+
+
+def _opt(a, dtype):
+    return None if a is None else np.ascontiguousarray(a, dtype=dtype)
+
+
+def _assemble(fn, N, group_begin, intra_ptr, intra_idx, intra_global, cross_ids, num_cross,
+              add_ptr, add_from, add_to):
+    """Shared driver of the two final-adjacency restatements: (row_ptr[N+1], col_idx)."""
+    G = group_begin.shape[0] - 2
+    ip, ii = _opt(intra_ptr, np.uint64), _opt(intra_idx, np.uint32)
+    cr = _opt(cross_ids, np.uint32)
+    stride = 0 if cr is None else (cr.shape[1] if cr.ndim == 2 else 1)
+    ap, af, at = _opt(add_ptr, np.uint32), _opt(add_from, np.uint32), _opt(add_to, np.uint32)
+    if ii is not None and ii.size == 0:
+        ii = np.zeros(1, np.uint32)
+    if af is not None and af.size == 0:
+        af, at = np.zeros(1, np.uint32), np.zeros(1, np.uint32)
+    row_ptr = np.zeros(N + 1, np.uint64)
+    p = lambda a: None if a is None else a.ctypes.data
+    gb = _u32(group_begin)
+    cap = 1 << 20
+    while True:
+        col = np.zeros(cap, np.uint32)
+        n = fn(N, G, p(gb), p(ip), p(ii), int(intra_global), p(None if cr is None else cr.reshape(-1)), stride,
+               num_cross, p(ap), p(af), p(at), p(row_ptr), p(col), cap)
+        if n >= 0:
+            return row_ptr, col[:n].copy()
+        cap *= 4
+
+
 class Oracle:
     """Plain-C restatement of the reference CPU semantics."""
 
@@ -89,6 +122,8 @@ class Oracle:
                                        _u32p, _f32p, C.c_int]
         L.ungo_additional_edges.restype = C.c_int64
         L.ungo_additional_edges.argtypes = _ADDL_ARGS
+        L.ungo_assemble_graph.restype = C.c_int64
+        L.ungo_assemble_graph.argtypes = _ASM_ARGS
         L.ungo_pack_anchor_row.restype = None
         L.ungo_pack_anchor_row.argtypes = [_u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                            C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
@@ -175,6 +210,11 @@ class Oracle:
         return _additional_edges(self.lib.ungo_additional_edges, X, group_begin, out_ptr, out_idx,
                                  cross_ids, num_cross)
 
+    def assemble_graph(self, N, group_begin, intra_ptr, intra_idx, intra_global, cross_ids, num_cross,
+                       add_ptr, add_from, add_to):
+        return _assemble(self.lib.ungo_assemble_graph, N, group_begin, intra_ptr, intra_idx, intra_global,
+                         cross_ids, num_cross, add_ptr, add_from, add_to)
+
     def pack_anchor_row(self, top_idx, cand_degree, n, local_src, final_degree, head_keep,
                         anchor_tail=1, anchor_slots=0, bidir_anchor=0, graph_stride=None):
         if graph_stride is None:
@@ -208,6 +248,10 @@ class RefOracle:
                                          _u32p, _f32p, C.c_int]
         L.ungref_additional_edges.restype = C.c_int64
         L.ungref_additional_edges.argtypes = _ADDL_ARGS
+        L.ungref_assemble_graph.restype = C.c_int64
+        L.ungref_assemble_graph.argtypes = _ASM_ARGS
+        L.ungref_graph_save.restype = None
+        L.ungref_graph_save.argtypes = [C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64), _u32p]
         self.lib = L
 
     def l2(self, a, b) -> float:
@@ -255,6 +299,17 @@ class RefOracle:
     def additional_edges(self, X, group_begin, out_ptr, out_idx, cross_ids, num_cross):
         return _additional_edges(self.lib.ungref_additional_edges, X, group_begin, out_ptr, out_idx,
                                  cross_ids, num_cross)
+
+    def assemble_graph(self, N, group_begin, intra_ptr, intra_idx, intra_global, cross_ids, num_cross,
+                       add_ptr, add_from, add_to):
+        return _assemble(self.lib.ungref_assemble_graph, N, group_begin, intra_ptr, intra_idx, intra_global,
+                         cross_ids, num_cross, add_ptr, add_from, add_to)
+
+    def graph_save(self, path, row_ptr, col_idx):
+        row_ptr = np.ascontiguousarray(row_ptr, np.uint64)
+        col = _u32(col_idx) if len(col_idx) else np.zeros(1, np.uint32)
+        self.lib.ungref_graph_save(str(path).encode(), row_ptr.shape[0] - 1,
+                                   row_ptr.ctypes.data_as(C.POINTER(C.c_uint64)), col)
 
 
 def ref_available() -> bool:

@@ -15,6 +15,10 @@
 //                          (src/uni_nav_graph_special_blocks.cpp:70-111)
 //   ungref_additional_edges -> build_cross_edges_generate_additional, exact branch
 //                          (src/uni_nav_graph_cross_edges.cpp:442-596)
+//   ungref_assemble_graph / ungref_graph_save -> the reference's own Graph/NeighborList
+//                          (include/graph.h) filled as add_offset_for_uni_nav_graph,
+//                          merge_cross_edges_to_graph and merge_additional_edges_to_graph
+//                          fill it, and its Graph::save
 // (their host file needs Boost and cannot be compiled here).
 #include <algorithm>
 #include <cmath>
@@ -25,6 +29,7 @@
 #include <omp.h>
 
 #include "distance.h"
+#include "graph.h"
 #include "search_queue.h"
 
 using ANNS::FloatL2DistanceHandler;
@@ -223,6 +228,65 @@ int64_t ungref_additional_edges(const float *X, uint32_t N, uint32_t dim, uint32
     if (needed)
         *needed = n;
     return n <= cap ? n : -1;
+}
+
+// The final adjacency in the reference's own container: intra edges as the group
+// graph builders leave them (local ids), add_offset_for_uni_nav_graph
+// (src/uni_nav_graph.cpp:285-297), then the writer's cross-edge append
+// (src/ung_cross_edge_output_writer.cpp:68-95, FlatId rows) and the additional-edge
+// merge (:30-42).  Exported as CSR; same contract as ung_assemble_graph_csr.
+int64_t ungref_assemble_graph(uint64_t N, uint32_t G, const uint32_t *group_begin, const uint64_t *intra_ptr,
+                              const uint32_t *intra_idx, int intra_global, const uint32_t *cross_ids,
+                              uint32_t cross_stride, uint32_t num_cross, const uint32_t *add_ptr,
+                              const uint32_t *add_from, const uint32_t *add_to, uint64_t *row_ptr,
+                              uint32_t *col_idx, int64_t cap)
+{
+    ANNS::Graph g((ANNS::IdxType)N);
+    std::vector<uint32_t> group_of(N);
+    for (uint32_t c = 1; c <= G; ++c)
+        for (uint32_t i = group_begin[c]; i < group_begin[c + 1]; ++i)
+            group_of[i] = c;
+    if (intra_ptr)
+        for (uint64_t i = 0; i < N; ++i)
+            for (uint64_t p = intra_ptr[i]; p < intra_ptr[i + 1]; ++p)
+                g.neighbors[i].emplace_back(intra_idx[p]);
+    if (!intra_global)
+        for (uint64_t i = 0; i < N; ++i)
+            for (auto &neighbor : g.neighbors[i])
+                neighbor += group_begin[group_of[i]];
+    if (cross_ids)
+        for (uint64_t i = 0; i < N; ++i)
+            for (uint32_t k = 0; k < num_cross; ++k) {
+                const uint32_t nb = cross_ids[i * cross_stride + k];
+                if (nb != std::numeric_limits<uint32_t>::max())
+                    g.neighbors[i].emplace_back(nb);
+            }
+    if (add_ptr)
+        for (uint32_t c = 1; c <= G; ++c)
+            for (uint32_t e = add_ptr[c]; e < add_ptr[c + 1]; ++e)
+                g.neighbors[add_from[e]].emplace_back(add_to[e]);
+    int64_t n = 0;
+    row_ptr[0] = 0;
+    for (uint64_t i = 0; i < N; ++i) {
+        for (auto nb : g.neighbors[i]) {
+            if (n < cap)
+                col_idx[n] = nb;
+            ++n;
+        }
+        row_ptr[i + 1] = (uint64_t)n;
+    }
+    return n <= cap ? n : -1;
+}
+
+// Graph::save of the reference (include/graph.h:207-216) on a CSR adjacency.
+void ungref_graph_save(const char *path, uint64_t N, const uint64_t *row_ptr, const uint32_t *col_idx)
+{
+    ANNS::Graph g((ANNS::IdxType)N);
+    for (uint64_t i = 0; i < N; ++i)
+        for (uint64_t p = row_ptr[i]; p < row_ptr[i + 1]; ++p)
+            g.neighbors[i].emplace_back(col_idx[p]);
+    std::string name(path);
+    g.save(name);
 }
 
 } // extern "C"

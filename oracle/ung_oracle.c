@@ -20,7 +20,12 @@
  *   ungo_intra_exact   vs oracle/_ref fixtures and a float64 brute force;
  *   ungo_divide_groups vs a Python dict-based first-appearance grouping;
  *   ungo_min_supersets vs a Python itertools enumeration of the definition;
- *   ungo_pack_anchor_row  vs hand-worked rows (small n) and invariants.
+ *   ungo_pack_anchor_row  vs hand-worked rows (small n) and invariants;
+ *   ungo_additional_edges vs golden fixtures and the restatement around the
+ *                      reference's own SearchQueue/distance (oracle/_ref), and vs
+ *                      closed-form edge counts;
+ *   ungo_assemble_graph vs the reference's own Graph/NeighborList filled by the
+ *                      reference's loops (oracle/_ref) and a hand-worked case.
  */
 #include "ung_oracle.h"
 
@@ -424,6 +429,61 @@ int64_t ungo_additional_edges(const float *X, uint32_t N, uint32_t dim, uint32_t
     free(qd);
     if (needed)
         *needed = n;
+    return n <= cap ? n : -1;
+}
+
+/* ---- final adjacency: uni_nav_graph.cpp:285-297, uni_nav_graph_cross_edges.cpp:849-868 ---- */
+
+typedef struct {
+    uint32_t *v;
+    uint64_t n, cap;
+} u32list;
+
+static void list_push(u32list *l, uint32_t x)
+{
+    if (l->n == l->cap) {
+        l->cap = l->cap ? 2 * l->cap : 8;
+        l->v = (uint32_t *)realloc(l->v, sizeof(uint32_t) * l->cap);
+    }
+    l->v[l->n++] = x;
+}
+
+int64_t ungo_assemble_graph(uint64_t N, uint32_t G, const uint32_t *group_begin, const uint64_t *intra_ptr,
+                            const uint32_t *intra_idx, int intra_global, const uint32_t *cross_ids,
+                            uint32_t cross_stride, uint32_t num_cross, const uint32_t *add_ptr,
+                            const uint32_t *add_from, const uint32_t *add_to, uint64_t *row_ptr,
+                            uint32_t *col_idx, int64_t cap)
+{
+    u32list *nb = (u32list *)calloc(N ? N : 1, sizeof(u32list));
+    for (uint32_t c = 1; c <= G; ++c)
+        for (uint64_t i = group_begin[c]; i < group_begin[c + 1]; ++i) {
+            if (intra_ptr) /* intra graph of the group (local ids), then add_offset */
+                for (uint64_t p = intra_ptr[i]; p < intra_ptr[i + 1]; ++p)
+                    list_push(&nb[i], intra_idx[p] + (intra_global ? 0u : group_begin[c]));
+        }
+    if (cross_ids)
+        for (uint64_t i = 0; i < N; ++i)
+            for (uint32_t t = 0; t < num_cross; ++t) {
+                const uint32_t x = cross_ids[i * cross_stride + t];
+                if (x != UINT32_MAX)
+                    list_push(&nb[i], x);
+            }
+    if (add_ptr)
+        for (uint32_t c = 1; c <= G; ++c)
+            for (uint32_t e = add_ptr[c]; e < add_ptr[c + 1]; ++e)
+                list_push(&nb[add_from[e]], add_to[e]);
+    int64_t n = 0;
+    row_ptr[0] = 0;
+    for (uint64_t i = 0; i < N; ++i) {
+        for (uint64_t j = 0; j < nb[i].n; ++j) {
+            if (n < cap)
+                col_idx[n] = nb[i].v[j];
+            ++n;
+        }
+        row_ptr[i + 1] = (uint64_t)n;
+        free(nb[i].v);
+    }
+    free(nb);
     return n <= cap ? n : -1;
 }
 

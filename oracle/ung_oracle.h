@@ -102,6 +102,19 @@ int64_t ungo_additional_edges(const float *X, uint32_t N, uint32_t dim, uint32_t
                               uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
                               uint32_t *edge_to, int64_t cap, int64_t *needed);
 
+/* Final adjacency, restating add_offset_for_uni_nav_graph (src/uni_nav_graph.cpp:285-297)
+ * followed by merge_cross_edges_to_graph / merge_additional_edges_to_graph
+ * (src/uni_nav_graph_cross_edges.cpp:849-868; writer src/ung_cross_edge_output_writer.cpp:
+ * 30-42, 68-95): row i = intra edges (+ the group's first id unless intra_global), the
+ * first num_cross FlatId entries of i (UINT32_MAX skipped), then i's additional edges in
+ * the order of the per-group lists.  Same contract as ung_assemble_graph_csr; returns
+ * the entry count or -1 when cap is too small. */
+int64_t ungo_assemble_graph(uint64_t N, uint32_t G, const uint32_t *group_begin, const uint64_t *intra_ptr,
+                            const uint32_t *intra_idx, int intra_global, const uint32_t *cross_ids,
+                            uint32_t cross_stride, uint32_t num_cross, const uint32_t *add_ptr,
+                            const uint32_t *add_from, const uint32_t *add_to, uint64_t *row_ptr,
+                            uint32_t *col_idx, int64_t cap);
+
 /* Exact intra-group top-K, restating build_exact_topk_graph_for_points
  * (src/uni_nav_graph_special_blocks.cpp:70-111): for every point i of the
  * group [begin, begin+n) the first min(K, n-1) local ids j != i ordered by

@@ -255,3 +255,40 @@ def test_additional_edges_cfg2_scaled(ctx, oracle):
     want = oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, ids, 6)
     _say(f"additional cfg2@60k: {got[1].size} edges")
     _assert_edges_equal(got, want, "cfg2@60k additional")
+
+
+def test_pipeline_graph_cfg1(cfg1_stage, oracle, tmp_path):
+    """The stage end to end on cfg1: cross edges, additional edges and the exact-anchor
+    batch on the GPU, assembled into the final CSR and saved as Graph::save text; the
+    same graph from the oracle's cross and additional edges (intra rows: the packed rows,
+    checked against the oracle by test_pack_cfg1_matches_oracle)."""
+    import copy
+    st = copy.copy(cfg1_stage)
+    st._ctx = None
+    st.gpu_prepare_all_vectors_on_device()
+    st.gpu_cross_groups_search_all_batched()
+    st.build_cross_edges_generate_additional()
+    batch = st.build_fast_exact_batch()
+    N = int(st.group_begin[-1])
+    gids = st.mid_groups()
+    deg = np.zeros(N, np.int64)
+    rows = {}
+    r = 0
+    for g in gids:
+        b, n = int(st.group_begin[g]), int(st.group_begin[g + 1] - st.group_begin[g])
+        for j in range(n):
+            row = batch.packed_graph[r + j]
+            rows[b + j] = row[1: 1 + row[0]]
+            deg[b + j] = row[0]
+        r += n
+    ip = np.zeros(N + 1, np.uint64)
+    ip[1:] = np.cumsum(deg)
+    ii = np.concatenate([rows[i] for i in sorted(rows)]).astype(np.uint32)
+    rp, ci = st.build_csr_adjacency(ip, ii)
+    cross, _, _ = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    add = oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, cross, 6)
+    wrp, wci = oracle.assemble_graph(N, st.group_begin, ip, ii, False, cross, 6, *add)
+    assert np.array_equal(rp, wrp) and np.array_equal(ci, wci)
+    st.save_graph(tmp_path / "graph")
+    assert (tmp_path / "graph").read_bytes().count(b"\n") == N
+    st.close()

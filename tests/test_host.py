@@ -145,3 +145,96 @@ def test_stage_mid_groups_router(cfg1_stage):
     mids = st.mid_groups()
     assert all(128 <= sizes[g - 1] <= 4096 for g in mids)
     assert len(mids) == int(((sizes >= 128) & (sizes <= 4096)).sum())
+
+
+# ---------------------------------------------------------------- output boundary
+def _graph_inputs(oracle, st, rng):
+    """Per-point intra lists (group-local ids): the exact K=32 lists for mid groups, a
+    complete graph for small groups and a few random local ids elsewhere; cross rows
+    from the oracle; additional edges from the oracle fed those rows."""
+    N = int(st.group_begin[-1])
+    sizes = np.diff(st.group_begin.astype(np.int64))[1:]
+    mids = set(st.mid_groups().tolist())
+    rows = [None] * N
+    for g in range(1, st.num_groups + 1):
+        b, n = int(st.group_begin[g]), int(sizes[g - 1])
+        if g in mids:
+            ids, _ = oracle.intra_exact(st.base, b, n, 32)
+            for j in range(n):
+                rows[b + j] = ids[j][ids[j] != 0xFFFFFFFF]
+        elif n <= 64:
+            for j in range(n):
+                rows[b + j] = np.array([t for t in range(n) if t != j], np.uint32)
+        else:
+            for j in range(n):
+                rows[b + j] = rng.choice(n, size=min(n - 1, 8), replace=False).astype(np.uint32)
+    ip = np.zeros(N + 1, np.uint64)
+    ip[1:] = np.cumsum([len(r) for r in rows])
+    ii = np.concatenate(rows).astype(np.uint32)
+    cross, _, _ = oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    add = oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, cross, 6)
+    return N, ip, ii, cross, add
+
+
+@pytest.mark.parametrize("intra_global", [False, True])
+def test_assemble_graph_matches_oracle(oracle, cfg1_stage, intra_global):
+    st = cfg1_stage
+    N, ip, ii, cross, add = _graph_inputs(oracle, st, np.random.default_rng(4))
+    if intra_global:  # group graphs already in global ids
+        base = np.zeros(N, np.uint32)
+        for g in range(1, st.num_groups + 1):
+            base[st.group_begin[g]: st.group_begin[g + 1]] = st.group_begin[g]
+        ii = (ii + np.repeat(base, np.diff(ip.astype(np.int64)))).astype(np.uint32)
+    got = F.assemble_graph_csr(N, st.group_begin, ip, ii, intra_global, cross, 6, *add, nthreads=4)
+    want = oracle.assemble_graph(N, st.group_begin, ip, ii, intra_global, cross, 6, *add)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    # rows: intra (global ids) + cross + additional, nothing else
+    deg = np.diff(got[0].astype(np.int64))
+    n_cross = (cross != 0xFFFFFFFF).sum(1)
+    n_add = np.bincount(add[1], minlength=N)
+    assert np.array_equal(deg, np.diff(ip.astype(np.int64)) + n_cross + n_add)
+
+
+def test_assemble_graph_matches_reference_container(oracle, ref_oracle, cfg1_stage):
+    st = cfg1_stage
+    N, ip, ii, cross, add = _graph_inputs(oracle, st, np.random.default_rng(5))
+    got = F.assemble_graph_csr(N, st.group_begin, ip, ii, False, cross, 6, *add)
+    want = ref_oracle.assemble_graph(N, st.group_begin, ip, ii, False, cross, 6, *add)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    # a shorter read of the FlatId rows (the writer reads topk_ entries)
+    got = F.assemble_graph_csr(N, st.group_begin, None, None, False, cross, 4, None, None, None)
+    want = ref_oracle.assemble_graph(N, st.group_begin, None, None, False, cross, 4, None, None, None)
+    assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+
+
+def test_assemble_graph_hand_worked():
+    gb = np.array([0, 0, 2, 3], np.uint32)           # group 1 = {0, 1}, group 2 = {2}
+    ip = np.array([0, 1, 2, 2], np.uint64)           # 0 -> local 1, 1 -> local 0
+    ii = np.array([1, 0], np.uint32)
+    cross = np.array([[2, 0xFFFFFFFF], [2, 0xFFFFFFFF], [0xFFFFFFFF, 0xFFFFFFFF]], np.uint32)
+    ap = np.array([0, 0, 2, 2], np.uint32)           # group 1: 1 -> 2, 0 -> 2
+    af = np.array([1, 0], np.uint32)
+    at = np.array([2, 2], np.uint32)
+    rp, ci = F.assemble_graph_csr(3, gb, ip, ii, False, cross, 2, ap, af, at)
+    assert rp.tolist() == [0, 3, 6, 6]
+    assert ci.tolist() == [1, 2, 2, 0, 2, 2]
+    with pytest.raises(F.UngHipError):  # an additional edge listed under the wrong group
+        F.assemble_graph_csr(3, gb, ip, ii, False, cross, 2, np.array([0, 0, 1, 2], np.uint32), af, at)
+
+
+def test_graph_save_text(tmp_path, ref_oracle, cfg1_stage):
+    rp = np.array([0, 2, 2, 5], np.uint64)
+    ci = np.array([7, 0, 1, 2, 123456], np.uint32)
+    F.graph_save_text(tmp_path / "g.txt", rp, ci)
+    assert (tmp_path / "g.txt").read_bytes() == b"0 7 0 \n1 \n2 1 2 123456 \n"
+    # byte-identical to the reference's own Graph::save on a real-sized graph
+    st = cfg1_stage
+    N = int(st.group_begin[-1])
+    rng = np.random.default_rng(6)
+    deg = rng.integers(0, 40, N)
+    rp = np.zeros(N + 1, np.uint64)
+    rp[1:] = np.cumsum(deg)
+    ci = rng.integers(0, N, int(rp[-1])).astype(np.uint32)
+    F.graph_save_text(tmp_path / "a.txt", rp, ci, nthreads=4)
+    ref_oracle.graph_save(tmp_path / "b.txt", rp, ci)
+    assert (tmp_path / "a.txt").read_bytes() == (tmp_path / "b.txt").read_bytes()
