@@ -43,6 +43,7 @@ class Stats(C.Structure):
         ("select_launches", C.c_uint64),
         ("fallback_rows", C.c_uint64),
         ("padded_pairs", C.c_uint64),
+        ("select_bytes", C.c_uint64),
     ]
 
     def as_dict(self) -> dict:

@@ -25,6 +25,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "ung_hip.h"
@@ -37,14 +38,16 @@ namespace {
 
 constexpr int BQ = 128;          // queries per work item (columns of the MFMA tiles)
 constexpr int BC = 128;          // candidates per tile (rows of the MFMA tiles)
-constexpr int KC = 32;           // k-chunk staged in LDS
-constexpr int LDSW = KC + 4;     // padded LDS row stride (floats)
+constexpr int KC = 32;           // k-chunk staged in LDS (dimensions)
+constexpr int LDSW = KC + 4;     // padded LDS row stride (32-bit words; a chunk row is 32 words)
 constexpr int NTHREADS = 256;    // 4 waves: 2 (candidate halves) x 2 (query halves)
 constexpr uint32_t SPLIT_V = 16384; // candidates per work item (raised so a job has <= 64 splits)
 constexpr uint32_t MAX_SPLITS = 64; // one wave lane per split in the merge
 constexpr uint32_t MERGE_ROWS = 4;  // result rows (one wave each) per merge block
 constexpr uint32_t MERGE_Q = 256;   // rows per packing block
 constexpr uint32_t NONE = 0xFFFFFFFFu;
+constexpr uint32_t FALLBACK_RANGE = 2048;      // fewest candidates per range of a flagged row's exact rescan
+constexpr uint32_t MAX_FALLBACK_SPLITS = 1024; // most ranges per flagged row
 
 struct Job {
     uint32_t q_begin, q_count;     // queries: global ids [q_begin, q_begin+q_count)
@@ -66,11 +69,13 @@ struct MergeItem {
 };
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct SelectParams {
-    const float *X;
+    const uint32_t *xs; // split base set: [N][dp] words, see ung_split_kernel
     const float *xn;
-    uint32_t d;
+    uint32_t dp;        // words per split row = d rounded up to a multiple of KC
     uint32_t k;
     const Job *jobs;
     const Item *items;
@@ -79,13 +84,13 @@ struct SelectParams {
     uint32_t *part_ids;
     float *part_dist;
     float *part_bound;
-    double eps_coef;  // 2*(d+4)*2^-24 : expansion-form error factor on (|q|+R)^2
+    double eps_coef;  // (7d/4+112)*2^-24 : expansion-form error factor on (|q|+R)^2
     double shrink;    // (d/8+8)*2^-24 : relative error of the reference summation
     double rmax;      // max candidate norm (slightly inflated)
     uint32_t n_items; // items of this launch
     uint32_t *item_ctr; // next item to take (zeroed before the launch)
     uint32_t lp;      // entries per partial row (approximate top-Lp)
-    uint32_t x_bytes; // bytes of X (buffer range of the 32-bit-offset kernels)
+    uint32_t x_bytes; // bytes of the split base set (buffer range of the 32-bit-offset kernels)
 };
 
 // ---------------------------------------------------------------------------
@@ -429,14 +434,13 @@ __device__ __forceinline__ void best_of_32(float (&d)[32], uint32_t (&id)[32], f
     }
 }
 
-// Operand loads (d % 4 == 0 for the two 16-byte modes):
-//   LOAD_BUF32 : X smaller than 4 GiB -- buffer loads with 32-bit byte offsets; the
-//                k-chunk advances a scalar offset, so the main loop spends no vector ALU
-//                work on addresses;
-//   LOAD_WIDE  : larger X -- queries through a buffer based at the item's first query
-//                row, candidates through 64-bit row pointers (one add per load);
-//   LOAD_SCALAR: any d -- 64-bit pointers with per-element bounds.
-enum : int { LOAD_SCALAR = 0, LOAD_BUF32 = 1, LOAD_WIDE = 2 };
+// Operand loads from the split base set (rows of dp words, every chunk whole):
+//   LOAD_BUF32 : split set smaller than 4 GiB -- buffer loads with 32-bit byte offsets;
+//                the k-chunk advances a scalar offset, so the main loop spends no vector
+//                ALU work on addresses;
+//   LOAD_WIDE  : larger -- queries through a buffer based at the item's first query
+//                row, candidates through 64-bit row pointers (one add per load).
+enum : int { LOAD_BUF32 = 1, LOAD_WIDE = 2 };
 
 template <int LT, int MODE, bool EXCL>
 __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
@@ -448,14 +452,16 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         return;
     const Item it = P.items[logical];
     const Job jb = P.jobs[it.job];
-    const uint32_t d = P.d;
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1;
     const int r = lane & 31, h = lane >> 5;
-    const uint32_t q0 = jb.q_begin + it.q_off;
-    const uint32_t qcnt = it.q_cnt;
-    const float *__restrict__ X = P.X;
+    // block-uniform values loaded with vector loads: readfirstlane keeps the query
+    // buffer descriptor of the wide mode in scalar registers
+    const uint32_t q0 = __builtin_amdgcn_readfirstlane(jb.q_begin + it.q_off);
+    const uint32_t qcnt = __builtin_amdgcn_readfirstlane(it.q_cnt);
+    const uint32_t dp = P.dp;
+    const uint32_t *__restrict__ XS = P.xs;
 
     if (tid < BQ)
         sm.qn[tid] = (uint32_t)tid < qcnt ? P.xn[q0 + tid] : 0.0f;
@@ -480,12 +486,11 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     const int c4 = (tid & 7) * 4;
     [[maybe_unused]] __amdgpu_buffer_rsrc_t qres, xres;
     [[maybe_unused]] uint32_t qoff[4], xoff[4];
-    [[maybe_unused]] const float *qrow[4];
-    [[maybe_unused]] const float *xrow[4];
+    [[maybe_unused]] const uint32_t *xrow[4];
     if constexpr (MODE == LOAD_BUF32) {
-        xres = __builtin_amdgcn_make_buffer_rsrc((void *)X, (short)0, (int)P.x_bytes, 0x00020000);
-    } else if constexpr (MODE == LOAD_WIDE) {
-        qres = __builtin_amdgcn_make_buffer_rsrc((void *)(X + (size_t)q0 * d), (short)0, (int)(qcnt * d * 4u),
+        xres = __builtin_amdgcn_make_buffer_rsrc((void *)XS, (short)0, (int)P.x_bytes, 0x00020000);
+    } else {
+        qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * dp), (short)0, (int)(qcnt * dp * 4u),
                                                  0x00020000);
     }
 #pragma unroll
@@ -493,11 +498,9 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         uint32_t ql = (uint32_t)(lr0 + 32 * m);
         ql = ql < qcnt ? ql : qcnt - 1;
         if constexpr (MODE == LOAD_BUF32)
-            qoff[m] = ((q0 + ql) * d + (uint32_t)c4) * 4u;
-        else if constexpr (MODE == LOAD_WIDE)
-            qoff[m] = (ql * d + (uint32_t)c4) * 4u;
+            qoff[m] = ((q0 + ql) * dp + (uint32_t)c4) * 4u;
         else
-            qrow[m] = X + (size_t)(q0 + ql) * d;
+            qoff[m] = (ql * dp + (uint32_t)c4) * 4u;
     }
 
     __syncthreads();
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     // across tile boundaries) into registers; the row-id table of tile t+1 is built
     // in ring slot (t+1)%3 while tile t computes.
     const uint32_t ntiles = (it.v_end - it.v_begin + BC - 1) / BC;
-    const uint32_t nk = (d + KC - 1) / KC;
+    const uint32_t nk = dp / KC;
     const uint32_t total = ntiles * nk;
 
     auto set_xrows = [&](int slot) {
@@ -520,82 +523,33 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
             uint32_t g = sm.rowid[slot][lr0 + 32 * m];
             g = (g == NONE) ? 0u : g; // padding rows load row 0 (their -|x|^2/2 is -inf)
             if constexpr (MODE == LOAD_BUF32)
-                xoff[m] = (g * d + (uint32_t)c4) * 4u;
-            else if constexpr (MODE == LOAD_WIDE)
-                xrow[m] = X + (size_t)g * d + c4;
+                xoff[m] = (g * dp + (uint32_t)c4) * 4u;
             else
-                xrow[m] = X + (size_t)g * d;
+                xrow[m] = XS + (size_t)g * dp + c4;
         }
     };
-    float4 rq[4], rx[4];
+    float4 rq[4], rx[4]; // raw split words (bf16 pairs), typed for 16-byte moves
     auto load_chunk = [&](uint32_t kc) {
-        if constexpr (MODE != LOAD_SCALAR) {
-            if (kc + KC <= d) {
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    if constexpr (MODE == LOAD_BUF32) {
-                        rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m], kc * 4u, 0));
-                        rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
-                    } else {
-                        rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff[m], kc * 4u, 0));
-                        rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + kc);
-                    }
-                }
-            } else { // ragged last chunk (d % 32 != 0): columns >= d read as zero
-                const bool ok = kc + (uint32_t)c4 < d;
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    rq[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    rx[m] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (ok) {
-                        if constexpr (MODE == LOAD_BUF32) {
-                            rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m] + kc * 4u, 0, 0));
-                            rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m] + kc * 4u, 0, 0));
-                        } else {
-                            rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff[m] + kc * 4u, 0, 0));
-                            rx[m] = *reinterpret_cast<const float4 *>(xrow[m] + kc);
-                        }
-                    }
-                }
-            }
-        } else {
-            const uint32_t col = kc + (uint32_t)c4;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                float tq[4], tx[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const bool ok = col + t < d;
-                    tq[t] = ok ? qrow[m][col + t] : 0.0f;
-                    tx[t] = ok ? xrow[m][col + t] : 0.0f;
-                }
-                rq[m] = make_float4(tq[0], tq[1], tq[2], tq[3]);
-                rx[m] = make_float4(tx[0], tx[1], tx[2], tx[3]);
+        for (int m = 0; m < 4; ++m) {
+            if constexpr (MODE == LOAD_BUF32) {
+                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m], kc * 4u, 0));
+                rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
+            } else {
+                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff[m], kc * 4u, 0));
+                rx[m] = __builtin_bit_cast(float4, *reinterpret_cast<const u32x4 *>(xrow[m] + kc));
             }
         }
     };
 
-    // accumulators start at -|x|^2/2 of their row, so after the k-loop
-    // acc = <x,q> - |x|^2/2 = -s  with  s = |x|^2/2 - <x,q>  (padding rows: -inf)
+    // accumulators start at 0 (the first chunk's MFMAs take C = 0) and hold <x,q> after
+    // the k-loop; the epilogue adds the row's -|x|^2/2 once, so acc = -s with
+    // s = |x|^2/2 - <x,q>  (padding rows: -inf).  Adding the norm term last keeps the
+    // running sums at the size of the products, which halves the accumulation error of
+    // the certified bound.
     floatx16 acc[2][2];
-    auto init_acc = [&](int slot) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                const float4 v = sm.nhx[slot][(wm * 64 + mb * 32 + 8 * g4 + 4 * h) >> 2];
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    acc[mb][nb][4 * g4 + 0] = v.x;
-                    acc[mb][nb][4 * g4 + 1] = v.y;
-                    acc[mb][nb][4 * g4 + 2] = v.z;
-                    acc[mb][nb][4 * g4 + 3] = v.w;
-                }
-            }
-    };
 
     __syncthreads(); // ring slot 0 and qn visible
-    init_acc(0);
     set_xrows(0);
     load_chunk(0);
 
@@ -620,26 +574,46 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                 load_chunk((kc + 1) * KC);
             }
         }
-        // 16 MFMA k-steps: step t covers dims kc*KC+t (lanes h=0) and kc*KC+16+t (h=1)
+        // The chunk's 32 dimensions as two k-blocks of 16; a panel row holds the bf16 high
+        // parts of the 32 dimensions (words 0..15) then the low parts (words 16..31).
+        // Lane half h feeds dimensions 16*kb + 8h .. +7 of block kb (8 bf16 = one float4),
+        // the same k order for the candidate (A) and query (B) operands.  Three passes per
+        // block: hi*hi, hi*lo, lo*hi (the dropped lo*lo term is within the error bound);
+        // pass-major order keeps four independent accumulators between dependent MFMAs.
+        // A tile's first MFMA of each accumulator takes C = 0 (no zeroing instructions).
+        auto mfma_chunk = [&](auto first_chunk) {
+            constexpr bool FIRST = decltype(first_chunk)::value;
+            const floatx16 zero = {};
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            const int kk = h * 4 + s4; // float4 column: dims 16h + 4*s4 .. +3
-            const float4 a0 = sm.u.p.xs[buf][wm * 64 + r][kk];
-            const float4 a1 = sm.u.p.xs[buf][wm * 64 + 32 + r][kk];
-            const float4 b0 = sm.u.p.qs[buf][wn * 64 + r][kk];
-            const float4 b1 = sm.u.p.qs[buf][wn * 64 + 32 + r][kk];
-            const float av0[4] = {a0.x, a0.y, a0.z, a0.w};
-            const float av1[4] = {a1.x, a1.y, a1.z, a1.w};
-            const float bv0[4] = {b0.x, b0.y, b0.z, b0.w};
-            const float bv1[4] = {b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[c], bv0[c], acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av0[c], bv1[c], acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[c], bv0[c], acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av1[c], bv1[c], acc[1][1], 0, 0, 0);
+            for (int kb = 0; kb < 2; ++kb) {
+                const int ch = 2 * kb + h; // float4 column of the high parts; +4: low parts
+                const bf16x8 ah0 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + r][ch]);
+                const bf16x8 ah1 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + 32 + r][ch]);
+                const bf16x8 bh0 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + r][ch]);
+                const bf16x8 bh1 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + 32 + r][ch]);
+                const bf16x8 al0 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + r][ch + 4]);
+                const bf16x8 al1 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + 32 + r][ch + 4]);
+                const bf16x8 bl0 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + r][ch + 4]);
+                const bf16x8 bl1 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + 32 + r][ch + 4]);
+                const bool z = FIRST && kb == 0;
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bh0, z ? zero : acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bh1, z ? zero : acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bh0, z ? zero : acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bh1, z ? zero : acc[1][1], 0, 0, 0);
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bl0, acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bl1, acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bl0, acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bl1, acc[1][1], 0, 0, 0);
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al0, bh0, acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al0, bh1, acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al1, bh0, acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al1, bh1, acc[1][1], 0, 0, 0);
             }
-        }
+        };
+        if (kc == 0)
+            mfma_chunk(std::true_type{});
+        else
+            mfma_chunk(std::false_type{});
         // next tile's row ids: issued after this step's MFMAs, visible after the next
         // step's barrier, consumed by the prefetch of the tile's first chunk
         if (nk > 1 && kc == 0 && tile + 1 < ntiles)
@@ -655,6 +629,18 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
             // other wave's of the previous tile).  Any candidate with a >= that value can
             // not be among the query's LT best (one queue already holds LT better ones),
             // and thresholds only decrease, so a stale value is safe.
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const float4 v = sm.nhx[slot][(wm * 64 + mb * 32 + 8 * g4 + 4 * h) >> 2];
+                    const float nh[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb)
+                            acc[mb][nb][4 * g4 + e] += nh[e];
+                }
             float tsh[2], ncth[2];
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
@@ -762,8 +748,6 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                 if (share && h == 0)
                     sm.tau[tile & 1][wm][wn * 64 + nb * 32 + r] = pair_t;
             }
-            if (tile + 1 < ntiles)
-                init_acc(next_slot);
             ++tile;
             kc = 0;
             slot = next_slot;
@@ -963,7 +947,10 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 }
 
 // ---------------------------------------------------------------------------
-// exact fallback: one wave per flagged row, persistent over the flagged list
+// exact fallback: every flagged row's union is cut into `splits` ranges; one wave scans
+// one (row, range) item (persistent over the items) and keeps its k best by (dist, id).
+// With one range the wave writes the result row; otherwise it writes a partial row and
+// ung_fallback_merge_kernel merges a row's ranges.
 // ---------------------------------------------------------------------------
 struct FallbackParams {
     const float *X;
@@ -974,6 +961,9 @@ struct FallbackParams {
     const uint32_t *seg_vend;
     const uint32_t *flag_count;
     const uint2 *flagged;
+    uint32_t splits;     // ranges per flagged row (1..MAX_FALLBACK_SPLITS)
+    uint32_t *part_ids;  // [flagged x splits x k] global ids (splits > 1)
+    float *part_dist;
     uint32_t *out_ids;
     float *out_dist;
     int32_t *out_size;
@@ -984,16 +974,21 @@ __global__ __launch_bounds__(64) void ung_fallback_kernel(FallbackParams F)
     __shared__ float sd[64][65];
     __shared__ uint32_t si[64][65];
     const int lane = threadIdx.x;
-    const uint32_t total = *F.flag_count;
+    const uint32_t S = F.splits;
+    const uint64_t total = (uint64_t)*F.flag_count * S;
     const uint32_t k = F.k;
-    for (uint32_t f = blockIdx.x; f < total; f += gridDim.x) {
+    for (uint64_t w = blockIdx.x; w < total; w += gridDim.x) {
+        const uint32_t f = (uint32_t)(w / S);
+        const uint32_t sp = (uint32_t)(w - (uint64_t)f * S);
         const uint2 fl = F.flagged[f];
         const Job jb = F.jobs[fl.x];
         const uint32_t q = jb.q_begin + fl.y;
         const bool excl = (jb.flags & 1u) != 0;
         const float *qv = F.X + (size_t)q * F.d;
+        const uint32_t v0 = (uint32_t)((uint64_t)jb.n_cand * sp / S);
+        const uint32_t v1 = (uint32_t)((uint64_t)jb.n_cand * (sp + 1) / S);
         int32_t size = 0;
-        for (uint32_t v = lane; v < jb.n_cand; v += 64) {
+        for (uint32_t v = v0 + (uint32_t)lane; v < v1; v += 64) {
             const uint32_t g = cand_id(F.seg_start, F.seg_vend, jb.seg_begin, jb.seg_count, v);
             if (excl && g == q)
                 continue;
@@ -1032,6 +1027,77 @@ __global__ __launch_bounds__(64) void ung_fallback_kernel(FallbackParams F)
             if (bi != NONE && hi == bi)
                 ++head;
             if (lane == 0) {
+                if (S == 1) {
+                    F.out_ids[orow * k + t] = bi != NONE ? bi - jb.id_base : NONE;
+                    if (F.out_dist)
+                        F.out_dist[orow * k + t] = bi != NONE ? bd : INFINITY;
+                } else {
+                    F.part_ids[w * k + t] = bi;
+                    F.part_dist[w * k + t] = bi != NONE ? bd : INFINITY;
+                }
+            }
+            count += bi != NONE ? 1u : 0u;
+        }
+        if (S == 1 && lane == 0 && F.out_size)
+            F.out_size[orow] = (int32_t)count;
+        __syncthreads();
+    }
+}
+
+// Merge of a flagged row's range results (ranges are disjoint, so ids are unique):
+// lane l first keeps the k best entries of ranges l, l+64, ... in its LDS queue, then
+// k rounds of a (dist, id) argmin over the lane heads.
+__global__ __launch_bounds__(64) void ung_fallback_merge_kernel(FallbackParams F)
+{
+    __shared__ float sd[64][65];
+    __shared__ uint32_t si[64][65];
+    const int lane = threadIdx.x;
+    const uint32_t S = F.splits, k = F.k;
+    const uint32_t total = *F.flag_count;
+    for (uint32_t f = blockIdx.x; f < total; f += gridDim.x) {
+        const uint2 fl = F.flagged[f];
+        const Job jb = F.jobs[fl.x];
+        const size_t orow = (size_t)jb.out_row + fl.y;
+        int32_t size = 0;
+        for (uint32_t sp = (uint32_t)lane; sp < S; sp += 64) {
+            const size_t base = ((size_t)f * S + sp) * k;
+            for (uint32_t t = 0; t < k; ++t) {
+                const uint32_t g = F.part_ids[base + t];
+                if (g == NONE)
+                    break; // a range's list is sorted, NONE entries come last
+                const float dist = F.part_dist[base + t];
+                if (size == (int32_t)k && !cand_less(dist, g, sd[lane][size - 1], si[lane][size - 1]))
+                    break; // the rest of this sorted list can not enter either
+                int32_t pos = size < (int32_t)k ? size : (int32_t)k - 1;
+                while (pos > 0 && cand_less(dist, g, sd[lane][pos - 1], si[lane][pos - 1])) {
+                    sd[lane][pos] = sd[lane][pos - 1];
+                    si[lane][pos] = si[lane][pos - 1];
+                    --pos;
+                }
+                sd[lane][pos] = dist;
+                si[lane][pos] = g;
+                if (size < (int32_t)k)
+                    ++size;
+            }
+        }
+        int head = 0;
+        uint32_t count = 0;
+        for (uint32_t t = 0; t < k; ++t) {
+            const float hd = head < size ? sd[lane][head] : INFINITY;
+            const uint32_t hi = head < size ? si[lane][head] : NONE;
+            float bd = hd;
+            uint32_t bi = hi;
+            for (int off = 32; off > 0; off >>= 1) {
+                const float od = __shfl_xor(bd, off);
+                const uint32_t oi = __shfl_xor(bi, off);
+                if (cand_less(od, oi, bd, bi)) {
+                    bd = od;
+                    bi = oi;
+                }
+            }
+            if (bi != NONE && hi == bi)
+                ++head;
+            if (lane == 0) {
                 F.out_ids[orow * k + t] = bi != NONE ? bi - jb.id_base : NONE;
                 if (F.out_dist)
                     F.out_dist[orow * k + t] = bi != NONE ? bd : INFINITY;
@@ -1047,8 +1113,44 @@ __global__ __launch_bounds__(64) void ung_fallback_kernel(FallbackParams F)
 // ---------------------------------------------------------------------------
 // small kernels
 // ---------------------------------------------------------------------------
+// bf16 bits of x rounded to nearest, ties to even (finite x).
+__device__ __forceinline__ uint32_t bf16_rne(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Split base set for the MFMA pre-selection: x = hi + lo + r with hi = bf16(x) and
+// lo = bf16(x - hi) (x - hi is exact: both lie within a factor 2 of each other), so
+// |r| <= 2^-18 |x|.  Row n holds dp words (dp = d rounded up to a multiple of KC); its
+// chunk c (dimensions 32c .. 32c+31) is 16 words of hi pairs then 16 words of lo pairs,
+// dimension 32c+2j in the low half of word j.  Dimensions >= d are zero.
+__global__ __launch_bounds__(256) void ung_split_kernel(const float *__restrict__ X, uint64_t N, uint32_t d,
+                                                        uint32_t dp, uint32_t *__restrict__ XS)
+{
+    const uint64_t per_row = dp / 2; // one (hi word, lo word) pair per thread
+    const uint64_t total = N * per_row;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t n = t / per_row;
+        const uint32_t w = (uint32_t)(t - n * per_row); // pair index within the row
+        const uint32_t c = w >> 4, j = w & 15u;
+        const uint32_t dim = 32u * c + 2u * j;
+        const float *x = X + n * d;
+        const float x0 = dim < d ? x[dim] : 0.0f;
+        const float x1 = dim + 1 < d ? x[dim + 1] : 0.0f;
+        const uint32_t h0 = bf16_rne(x0), h1 = bf16_rne(x1);
+        const uint32_t l0 = bf16_rne(x0 - __uint_as_float(h0 << 16));
+        const uint32_t l1 = bf16_rne(x1 - __uint_as_float(h1 << 16));
+        uint32_t *row = XS + n * dp + 32u * c;
+        row[j] = h0 | (h1 << 16);
+        row[16 + j] = l0 | (l1 << 16);
+    }
+}
+
 // Squared norms (one wave per row, grid-stride over rows; lanes stride the row) and the
-// largest of them: a block-wide maximum, then one atomic per block.
+// largest of them: a block-wide maximum, then one atomic per block.  Accumulated in fp64
+// and rounded once, so each cached norm is within 2^-24 (relative) of |x|^2.
 __global__ __launch_bounds__(256) void ung_norm_kernel(const float *__restrict__ X, uint64_t N, uint32_t d,
                                                        float *__restrict__ xn, unsigned int *__restrict__ maxbits)
 {
@@ -1058,11 +1160,12 @@ __global__ __launch_bounds__(256) void ung_norm_kernel(const float *__restrict__
     unsigned int mx = 0u; // non-negative floats order as their bit patterns
     for (uint64_t row = (uint64_t)blockIdx.x * 4u + (uint64_t)wave; row < N; row += nwaves) {
         const float *x = X + row * d;
-        float s = 0.0f;
+        double sd = 0.0;
         for (uint32_t t = lane; t < d; t += 64)
-            s = __builtin_fmaf(x[t], x[t], s);
+            sd = __builtin_fma((double)x[t], (double)x[t], sd);
         for (int off = 32; off > 0; off >>= 1)
-            s += __shfl_xor(s, off);
+            sd += __shfl_xor(sd, off);
+        const float s = (float)sd;
         if (lane == 0)
             xn[row] = s;
         mx = max(mx, __float_as_uint(s));
@@ -1208,13 +1311,18 @@ __global__ void ung_mfma_probe_kernel(float *out)
 {
     const int lane = threadIdx.x;
     const int r = lane & 31, h = lane >> 5;
-    // A[m][k] = m + 0.5*k ; B[k][n] = (k+1) * (n - 7)
-    const float a = (float)r + 0.5f * (float)h;
-    const float b = (float)(h + 1) * (float)(r - 7);
+    // A[m][k] = (m - 16) + (k % 8) / 4 ; B[k][n] = (k % 4 + 1) * (n - 7): exact in bf16,
+    // products and sums exact in fp32.  Lane (r, h) feeds k = 8h + j of row/column r.
+    bf16x8 a, b;
+    for (int j = 0; j < 8; ++j) {
+        const int kk = 8 * h + j;
+        a[j] = (__bf16)((float)(r - 16) + 0.25f * (float)(kk % 8));
+        b[j] = (__bf16)((float)(kk % 4 + 1) * (float)(r - 7));
+    }
     floatx16 acc;
     for (int i = 0; i < 16; ++i)
         acc[i] = 0.0f;
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
     for (int i = 0; i < 16; ++i) {
         const int row = 8 * (i >> 2) + 4 * h + (i & 3);
         out[row * 32 + r] = acc[i];
@@ -1307,6 +1415,8 @@ struct ung_hip_ctx {
     hipEvent_t ev[8] = {};
     // resident base set
     float *X = nullptr;
+    uint32_t *XS = nullptr; // split base set (bf16 hi/lo pairs) for the MFMA pre-selection
+    uint32_t dp = 0;        // its row pitch in words
     float *xn = nullptr;
     unsigned int *maxbits = nullptr;
     uint64_t N = 0;
@@ -1322,6 +1432,8 @@ struct ung_hip_ctx {
     DevBuf<float> part_bound;
     DevBuf<uint32_t> flag_count;
     DevBuf<uint2> flagged;
+    DevBuf<uint32_t> fb_ids; // fallback range results
+    DevBuf<float> fb_dist;
     // results
     ResultBufs cross;
     ResultBufs group;
@@ -1337,6 +1449,9 @@ struct ung_hip_ctx {
     DevBuf<int32_t> a_size;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
     bool force_wide = false;
+    // test hook: UNG_HIP_EPS_SCALE=s (s >= 1) at create widens the certification error
+    // bound by s, which sends more rows (all, for a huge s) through the exact rescan
+    double eps_scale = 1.0;
 };
 
 namespace {
@@ -1411,11 +1526,9 @@ int pick_lt(uint32_t k)
 template <int LT>
 int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, bool excl)
 {
-    // 16-byte loads need d % 4 == 0; 32-bit buffer offsets a base set below 4 GiB
-    const uint64_t x_bytes = (uint64_t)ctx->N * ctx->d * sizeof(float);
-    const int mode = (ctx->d % 4) != 0                                  ? LOAD_SCALAR
-                     : (x_bytes < (1ull << 32) && !ctx->force_wide) ? LOAD_BUF32
-                                                                      : LOAD_WIDE;
+    // 32-bit buffer offsets need a split base set below 4 GiB
+    const uint64_t x_bytes = (uint64_t)ctx->N * ctx->dp * sizeof(uint32_t);
+    const int mode = (x_bytes < (1ull << 32) && !ctx->force_wide) ? LOAD_BUF32 : LOAD_WIDE;
     // grid dimension x is limited to 2^31-1; chunk the item list
     const uint32_t max_grid = 1u << 30;
     for (uint32_t off = 0; off < n_items; off += max_grid) {
@@ -1433,17 +1546,34 @@ int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, b
             hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true>), g, b, 0, ctx->stream, Q);
         else if (mode == LOAD_BUF32)
             hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false>), g, b, 0, ctx->stream, Q);
-        else if (mode == LOAD_WIDE && excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true>), g, b, 0, ctx->stream, Q);
-        else if (mode == LOAD_WIDE)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false>), g, b, 0, ctx->stream, Q);
         else if (excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_SCALAR, true>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true>), g, b, 0, ctx->stream, Q);
         else
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_SCALAR, false>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false>), g, b, 0, ctx->stream, Q);
         HIPCHECK(hipGetLastError());
     }
     return UNG_HIP_OK;
+}
+
+// Error factor of the expansion-form value a = fl(|q|^2 - 2*acc) of the select kernel:
+// |a - D| <= eps_coef * (|q| + R)^2 with D the exact squared distance, u = 2^-24.
+//  * norm caches fl(|x|^2), fl(|q|^2): fp64 sums rounded once, <= u relative each
+//                                                                     -> u (|q|+R)^2
+//  * split operands: each product x_i q_i is replaced by hi*hi + hi*lo + lo*hi, exact in
+//    fp32 (8-bit significands); the dropped terms are <= 3.01 * 2^-18 |x_i q_i|, so <=
+//    192.6 u |x||q| in s and 385.2 u |x||q| <= 96.3 u (|q|+R)^2 in a
+//  * accumulation of the 3d products from 0 (sum of |products| <= 1.0079 |x||q|): with
+//    round-to-nearest additions in any order <= 3d*u*1.0079 |x||q|; a fused adder that
+//    truncates each of its 17 operands by at most one ulp of the largest and rounds once
+//    gives <= 17u per MFMA over 3d/16 MFMAs, 3.19 d*u*1.0079 |x||q|.  In a: <= 1.61 d*u
+//    (|q|+R)^2
+//  * adding -fl(|x|^2)/2 (one rounding) and the final fma: <= 2.01 u (|q|+R)^2
+// Sum <= (1.61 d + 99.4) u (|q|+R)^2; the factor below keeps a margin.  Flushed bf16 or
+// fp32 subnormals add at most ~6d * 2^-126 absolute, covered by the 1e-30 term of
+// lower_bound_exact.
+double eps_coef_for(uint32_t d)
+{
+    return (1.75 * (double)d + 112.0) * std::ldexp(1.0, -24);
 }
 
 // Runs a planned job list; results into `res` (rows x k), rows of res already
@@ -1486,9 +1616,9 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
     HIPCHECK(hipEventRecord(ctx->ev[0], ctx->stream));
 
     SelectParams P{};
-    P.X = ctx->X;
+    P.xs = ctx->XS;
     P.xn = ctx->xn;
-    P.d = ctx->d;
+    P.dp = ctx->dp;
     P.k = k;
     P.jobs = ctx->jobs.p;
     P.items = ctx->items.p;
@@ -1497,7 +1627,7 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
     P.part_ids = ctx->part_ids.p;
     P.part_dist = ctx->part_dist.p;
     P.part_bound = ctx->part_bound.p;
-    P.eps_coef = 2.0 * ((double)ctx->d + 4.0) * std::ldexp(1.0, -24);
+    P.eps_coef = eps_coef_for(ctx->d) * ctx->eps_scale;
     P.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
     P.rmax = ctx->rmax;
     P.item_ctr = ctx->flag_count.p + 1;
@@ -1542,26 +1672,47 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
         HIPCHECK(hipGetLastError());
     }
     HIPCHECK(hipEventRecord(ctx->ev[2], ctx->stream));
-
-    FallbackParams F{};
-    F.X = ctx->X;
-    F.d = ctx->d;
-    F.k = k;
-    F.jobs = ctx->jobs.p;
-    F.seg_start = ctx->seg_start.p;
-    F.seg_vend = ctx->seg_vend.p;
-    F.flag_count = ctx->flag_count.p;
-    F.flagged = ctx->flagged.p;
-    F.out_ids = res.ids.p;
-    F.out_dist = res.dist.p;
-    F.out_size = res.size.p;
-    hipLaunchKernelGGL(ung_fallback_kernel, dim3(512), dim3(64), 0, ctx->stream, F);
-    HIPCHECK(hipGetLastError());
+    uint32_t nflag = 0;
+    HIPCHECK(hipMemcpyAsync(&nflag, ctx->flag_count.p, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    if (nflag > 0) {
+        // a flagged row's union is cut into ranges of >= FALLBACK_RANGE candidates
+        uint64_t max_cand = 0;
+        for (const Job &jb : pl.jobs)
+            max_cand = std::max<uint64_t>(max_cand, jb.n_cand);
+        const uint32_t S =
+            (uint32_t)std::min<uint64_t>(MAX_FALLBACK_SPLITS, std::max<uint64_t>(1, max_cand / FALLBACK_RANGE));
+        FallbackParams F{};
+        F.X = ctx->X;
+        F.d = ctx->d;
+        F.k = k;
+        F.jobs = ctx->jobs.p;
+        F.seg_start = ctx->seg_start.p;
+        F.seg_vend = ctx->seg_vend.p;
+        F.flag_count = ctx->flag_count.p;
+        F.flagged = ctx->flagged.p;
+        F.splits = S;
+        F.out_ids = res.ids.p;
+        F.out_dist = res.dist.p;
+        F.out_size = res.size.p;
+        if (S > 1) {
+            if ((rc = ctx->fb_ids.ensure((uint64_t)nflag * S * k)) || (rc = ctx->fb_dist.ensure((uint64_t)nflag * S * k)))
+                return rc;
+            F.part_ids = ctx->fb_ids.p;
+            F.part_dist = ctx->fb_dist.p;
+        }
+        const uint64_t items = (uint64_t)nflag * S;
+        hipLaunchKernelGGL(ung_fallback_kernel, dim3((unsigned)std::min<uint64_t>(items, 1u << 20)), dim3(64), 0,
+                           ctx->stream, F);
+        HIPCHECK(hipGetLastError());
+        if (S > 1) {
+            hipLaunchKernelGGL(ung_fallback_merge_kernel, dim3(std::min<uint32_t>(nflag, 8192u)), dim3(64), 0,
+                               ctx->stream, F);
+            HIPCHECK(hipGetLastError());
+        }
+    }
     HIPCHECK(hipEventRecord(ctx->ev[3], ctx->stream));
     HIPCHECK(hipEventSynchronize(ctx->ev[3]));
-
-    uint32_t nflag = 0;
-    HIPCHECK(hipMemcpy(&nflag, ctx->flag_count.p, sizeof(uint32_t), hipMemcpyDeviceToHost));
     if (st) {
         float a = 0, b = 0, c = 0;
         HIPCHECK(hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[1]));
@@ -1574,6 +1725,10 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
         st->fallback_rows += nflag;
         st->pairs += pl.pairs;
         st->padded_pairs += pl.padded;
+        uint64_t rows_streamed = 0;
+        for (const Item &it : pl.items)
+            rows_streamed += (uint64_t)it.q_cnt + (it.v_end - it.v_begin);
+        st->select_bytes += rows_streamed * ctx->dp * sizeof(uint32_t);
         st->rows += pl.rows;
         st->work_items += pl.items.size();
         st->select_launches += 1;
@@ -1927,6 +2082,7 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         F.seg_vend = ctx->seg_vend.p;
         F.flag_count = ctx->flag_count.p;
         F.flagged = ctx->flagged.p;
+        F.splits = 1;
         F.out_ids = ctx->a_ids.p;
         F.out_dist = nullptr;
         F.out_size = ctx->a_size.p;
@@ -2010,7 +2166,9 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
         return rc;
     ung_hip_release_vectors(ctx);
     const auto t0 = clk::now();
+    const uint32_t dp = (dim + KC - 1) / KC * KC;
     HIPCHECK(hipMalloc((void **)&ctx->X, N * dim * sizeof(float)));
+    HIPCHECK(hipMalloc((void **)&ctx->XS, N * dp * sizeof(uint32_t)));
     HIPCHECK(hipMalloc((void **)&ctx->xn, N * sizeof(float)));
     HIPCHECK(hipMalloc((void **)&ctx->maxbits, sizeof(unsigned int)));
     HIPCHECK(hipMemcpyAsync(ctx->X, src, N * dim * sizeof(float),
@@ -2024,6 +2182,10 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
     hipLaunchKernelGGL(ung_norm_kernel, dim3((unsigned)norm_blocks), dim3(256), 0, ctx->stream, ctx->X, N, dim,
                        ctx->xn, ctx->maxbits);
     HIPCHECK(hipGetLastError());
+    const uint64_t split_blocks = std::min<uint64_t>((N * (dp / 2) + 255) / 256, 16384);
+    hipLaunchKernelGGL(ung_split_kernel, dim3((unsigned)split_blocks), dim3(256), 0, ctx->stream, ctx->X, N, dim, dp,
+                       ctx->XS);
+    HIPCHECK(hipGetLastError());
     HIPCHECK(hipEventRecord(ctx->ev[5], ctx->stream));
     unsigned int mb = 0;
     HIPCHECK(hipMemcpyAsync(&mb, ctx->maxbits, sizeof(mb), hipMemcpyDeviceToHost, ctx->stream));
@@ -2032,6 +2194,7 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
     std::memcpy(&mxf, &mb, sizeof(mxf));
     ctx->N = N;
     ctx->d = dim;
+    ctx->dp = dp;
     // max norm, inflated for the rounding of the norm cache
     ctx->rmax = std::sqrt((double)mxf * (1.0 + 1e-5)) * (1.0 + 1e-6);
     ctx->cross.valid = false;
@@ -2053,7 +2216,7 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
 // ---------------------------------------------------------------------------
 extern "C" {
 
-const char *ung_hip_version(void) { return "ung_hip 0.1 (gfx950, fp32 MFMA select + exact re-rank)"; }
+const char *ung_hip_version(void) { return "ung_hip 0.2 (gfx950, split-bf16 MFMA pre-select + exact fp32 re-rank)"; }
 
 int ung_hip_create(int device, ung_hip_ctx **out)
 {
@@ -2074,6 +2237,10 @@ int ung_hip_create(int device, ung_hip_ctx **out)
     ctx->device = device;
     if (const char *s = std::getenv("UNG_HIP_FORCE_WIDE"))
         ctx->force_wide = s[0] == '1';
+    if (const char *s = std::getenv("UNG_HIP_EPS_SCALE")) {
+        const double v = std::atof(s);
+        ctx->eps_scale = v >= 1.0 ? v : 1.0; // a smaller bound would not be an error bound
+    }
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
         set_error("hipStreamCreateWithFlags failed: %s", hipGetErrorString(e));
@@ -2104,11 +2271,15 @@ int ung_hip_release_vectors(ung_hip_ctx *ctx)
         (void)hipStreamSynchronize(ctx->stream);
     if (ctx->X)
         (void)hipFree(ctx->X);
+    if (ctx->XS)
+        (void)hipFree(ctx->XS);
     if (ctx->xn)
         (void)hipFree(ctx->xn);
     if (ctx->maxbits)
         (void)hipFree(ctx->maxbits);
     ctx->X = nullptr;
+    ctx->XS = nullptr;
+    ctx->dp = 0;
     ctx->xn = nullptr;
     ctx->maxbits = nullptr;
     ctx->N = 0;
@@ -2134,6 +2305,8 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     ctx->part_bound.release();
     ctx->flag_count.release();
     ctx->flagged.release();
+    ctx->fb_ids.release();
+    ctx->fb_dist.release();
     ctx->cross.release();
     ctx->group.release();
     ctx->gjobs.release();
@@ -2389,8 +2562,8 @@ int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err)
     for (int m = 0; m < 32; ++m)
         for (int n = 0; n < 32; ++n) {
             double ref = 0;
-            for (int kk = 0; kk < 2; ++kk)
-                ref += ((double)m + 0.5 * kk) * ((double)(kk + 1) * (double)(n - 7));
+            for (int kk = 0; kk < 16; ++kk)
+                ref += ((double)(m - 16) + 0.25 * (kk % 8)) * ((double)(kk % 4 + 1) * (double)(n - 7));
             mx = std::max(mx, std::fabs(ref - (double)host[m * 32 + n]));
         }
     *max_abs_err = mx;

@@ -60,6 +60,9 @@ typedef struct ung_hip_stats {
     uint64_t fallback_rows;  /* rows whose MFMA pre-selection could not be certified
                                 and were rescanned exactly */
     uint64_t padded_pairs;   /* pairs computed by the MFMA tiles incl. padding */
+    uint64_t select_bytes;   /* operand bytes the select kernel(s) stream: per work item,
+                                its query rows and its candidate rows of the split base
+                                set (4 * dp bytes a row, dp = dim rounded up to 32) */
 } ung_hip_stats;
 
 /* Message of the calling thread's last failure ("" if none). */
