@@ -304,21 +304,68 @@ __device__ __forceinline__ float s_bound(float thr, float qn)
     return 0.5f * (thr - qn) + 0x1p-20f * (fabsf(thr) + fabsf(qn));
 }
 
-// Fills the row-id ring slot for the candidate tile starting at virtual index v0.
-__device__ __forceinline__ void build_rowids(SelectSmem &sm, int slot, const SelectParams &P, const Job &jb,
-                                             uint32_t v0, uint32_t v_end, int tid)
+// Position of a row thread in the job's segment list.  The thread's virtual index only
+// grows (tile after tile), so the segment is found by a forward step: no memory access
+// inside the current segment, one load on entering the next one, a binary search over
+// the rest only when a tile skips whole segments.
+struct RowCursor {
+    uint32_t seg = 0xFFFFFFFFu; // current segment (none yet)
+    uint32_t vend = 0;          // its virtual end
+    uint32_t base = 0;          // global id = base + v inside it (mod 2^32)
+};
+
+// Global id of virtual candidate v (v < the job's union size, v >= any earlier v).
+__device__ __forceinline__ uint32_t cursor_id(RowCursor &c, const SelectParams &P, const Job &jb, uint32_t v)
 {
+    if (v >= c.vend) {
+        const uint32_t *__restrict__ ve = P.seg_vend + jb.seg_begin;
+        uint32_t lo = c.seg + 1u, vstart = c.vend;
+        uint32_t e = ve[lo];
+        if (e <= v) {
+            // first segment in [lo+1, seg_count) ending after v; the last one ends at
+            // the union size > v
+            uint32_t hi = jb.seg_count - 1u;
+            ++lo;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (ve[mid] > v)
+                    hi = mid;
+                else
+                    lo = mid + 1u;
+            }
+            vstart = ve[lo - 1u];
+            e = ve[lo];
+        }
+        c.seg = lo;
+        c.vend = e;
+        c.base = P.seg_start[jb.seg_begin + lo] - vstart;
+    }
+    return c.base + v;
+}
+
+// Row ids of the candidate tile starting at virtual index v0 into ring slot `slot`;
+// returns the row's |x|^2 (+inf for padding rows), a load the caller consumes later
+// (finish_rowids), so its latency overlaps other work.
+__device__ __forceinline__ float start_rowids(SelectSmem &sm, int slot, RowCursor &cur, const SelectParams &P,
+                                              const Job &jb, uint32_t v0, uint32_t v_end, int tid)
+{
+    float nx = INFINITY;
     if (tid < BC) {
         const uint32_t v = v0 + (uint32_t)tid;
         uint32_t g = NONE;
-        float nx = INFINITY;
         if (v < v_end) {
-            g = cand_id(P.seg_start, P.seg_vend, jb.seg_begin, jb.seg_count, v);
+            g = cursor_id(cur, P, jb, v);
             nx = P.xn[g];
         }
         sm.rowid[slot][tid] = g;
-        reinterpret_cast<float *>(sm.nhx[slot])[tid] = -0.5f * nx; // -|x|^2/2 (exact scaling)
     }
+    return nx;
+}
+
+__device__ __forceinline__ void finish_rowids(SelectSmem &sm, int slot, float nx, int tid)
+{
+    if (tid < BC)
+        reinterpret_cast<float *>(sm.nhx[slot])[tid] = -0.5f * nx; // -|x|^2/2 (exact scaling)
 }
 
 // Tile row (0..127) of a lane's j-th value of one query column, j = 16*mb + i of
@@ -465,7 +512,8 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 
     if (tid < BQ)
         sm.qn[tid] = (uint32_t)tid < qcnt ? P.xn[q0 + tid] : 0.0f;
-    build_rowids(sm, 0, P, jb, it.v_begin, it.v_end, tid);
+    RowCursor cur;
+    finish_rowids(sm, 0, start_rowids(sm, 0, cur, P, jb, it.v_begin, it.v_end, tid), tid);
 
     float ld[2][LT];
     uint32_t li[2][LT];
@@ -485,7 +533,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     const int lr0 = tid >> 3;
     const int c4 = (tid & 7) * 4;
     [[maybe_unused]] __amdgpu_buffer_rsrc_t qres, xres;
-    [[maybe_unused]] uint32_t qoff[4], xoff[4];
+    [[maybe_unused]] uint32_t xoff[4];
     [[maybe_unused]] const uint32_t *xrow[4];
     if constexpr (MODE == LOAD_BUF32) {
         xres = __builtin_amdgcn_make_buffer_rsrc((void *)XS, (short)0, (int)P.x_bytes, 0x00020000);
@@ -493,15 +541,12 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * dp), (short)0, (int)(qcnt * dp * 4u),
                                                  0x00020000);
     }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        uint32_t ql = (uint32_t)(lr0 + 32 * m);
-        ql = ql < qcnt ? ql : qcnt - 1;
-        if constexpr (MODE == LOAD_BUF32)
-            qoff[m] = ((q0 + ql) * dp + (uint32_t)c4) * 4u;
-        else
-            qoff[m] = (ql * dp + (uint32_t)c4) * 4u;
-    }
+    // query rows lr0 + 32m: one vector offset, the 32-row steps as scalar offsets.  Rows
+    // past the item's queries (padding columns, whose results are never read) load
+    // whatever the buffer holds there, zero beyond its range.
+    const uint32_t qrow_step = 32u * dp * 4u;
+    const uint32_t qoff = MODE == LOAD_BUF32 ? ((q0 + (uint32_t)lr0) * dp + (uint32_t)c4) * 4u
+                                             : ((uint32_t)lr0 * dp + (uint32_t)c4) * 4u;
 
     __syncthreads();
     float qnv[2];
@@ -533,10 +578,10 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             if constexpr (MODE == LOAD_BUF32) {
-                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff[m], kc * 4u, 0));
+                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
             } else {
-                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff[m], kc * 4u, 0));
+                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, *reinterpret_cast<const u32x4 *>(xrow[m] + kc));
             }
         }
@@ -555,6 +600,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 
     uint32_t tile = 0, kc = 0;
     int slot = 0;
+    float pend_nx = INFINITY;
     for (uint32_t s = 0; s < total; ++s) {
         const int buf = (int)(s & 1u);
         const int next_slot = slot == 2 ? 0 : slot + 1;
@@ -564,7 +610,11 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
             sm.u.p.xs[buf][lr0 + 32 * m][c4 >> 2] = rx[m];
         }
         if (nk == 1 && tile + 1 < ntiles)
-            build_rowids(sm, next_slot, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
+            finish_rowids(sm, next_slot,
+                          start_rowids(sm, next_slot, cur, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid), tid);
+        // |x|^2 of the next tile's rows, loaded during the previous step
+        if (nk > 1 && kc == 1 && tile + 1 < ntiles)
+            finish_rowids(sm, next_slot, pend_nx, tid);
         __syncthreads();
         if (s + 1 < total) {
             if (kc + 1 == nk) {
@@ -615,9 +665,10 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         else
             mfma_chunk(std::false_type{});
         // next tile's row ids: issued after this step's MFMAs, visible after the next
-        // step's barrier, consumed by the prefetch of the tile's first chunk
+        // step's barrier, consumed by the prefetch of the tile's first chunk (at step
+        // nk-1 >= 1); the |x|^2 values are stored at the top of step 1
         if (nk > 1 && kc == 0 && tile + 1 < ntiles)
-            build_rowids(sm, next_slot, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
+            pend_nx = start_rowids(sm, next_slot, cur, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
 
         if (kc + 1 == nk) {
             // epilogue: acc[mb][nb][i] = -s for row tile_row(wm, h, 16*mb + i) and query
