@@ -18,6 +18,7 @@
 // src/distance.cpp:34-91 (distance rounding), src/search_queue.cpp:26-53
 // ((dist,id) order), src/tagore_graph_builder.cu:727-794 (anchor packing).
 #include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <chrono>
@@ -909,13 +910,16 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
     const uint32_t q = jb.q_begin + ql;
     const uint32_t S = jb.n_split, Lp = M.lp, k = M.k;
 
-    uint32_t ci = NONE; // lane t < Lp: the t-th smallest approximate candidate
-    float B;            // approximate-space bound of every candidate left out
+    // slot h of lane t holds the (64h + t)-th smallest approximate candidate (Lp <= 128)
+    uint32_t ci[2] = {NONE, NONE};
+    float B; // approximate-space bound of every candidate left out
     if (S == 1) {
         // one split: its partial row is already the approximate top-Lp
         const size_t prow = (size_t)jb.part_base + ql;
-        if ((uint32_t)lane < Lp)
-            ci = M.part_ids[prow * Lp + lane];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            if ((uint32_t)(64 * h + lane) < Lp)
+                ci[h] = M.part_ids[prow * Lp + 64 * h + lane];
         B = M.part_bound[prow];
     } else {
         size_t prow = 0;
@@ -943,8 +947,12 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
                 a_next = bd;
                 break;
             }
-            if ((uint32_t)lane == t)
-                ci = bi;
+            if ((uint32_t)lane == (t & 63u)) {
+                if (t < 64)
+                    ci[0] = bi;
+                else
+                    ci[1] = bi;
+            }
             if (hi == bi) {
                 ++pos;
                 if (pos < Lp) {
@@ -959,25 +967,38 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
         B = fminf(bmin, a_next);
     }
 
-    // exact re-score, one lane per candidate
+    // exact re-score, one lane per candidate and slot
     const float *qv = M.X + (size_t)q * M.d;
-    float ex = INFINITY;
-    if (ci != NONE)
-        ex = l2_ref_lane(qv, M.X + (size_t)ci * M.d, M.d);
-    // rank under (exact, id, lane)
-    uint32_t rank = 0;
+    float ex[2] = {INFINITY, INFINITY};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (ci[h] != NONE)
+            ex[h] = l2_ref_lane(qv, M.X + (size_t)ci[h] * M.d, M.d);
+    // rank under (exact, id, position)
+    uint32_t rank[2] = {0u, 0u};
     for (uint32_t f = 0; f < Lp; ++f) {
-        const float df = __shfl(ex, (int)f);
-        const uint32_t idf = __shfl(ci, (int)f);
-        rank += (df < ex || (df == ex && (idf < ci || (idf == ci && f < (uint32_t)lane)))) ? 1u : 0u;
+        const int src = (int)(f & 63u);
+        const float df = f < 64 ? __shfl(ex[0], src) : __shfl(ex[1], src);
+        const uint32_t idf = f < 64 ? __shfl(ci[0], src) : __shfl(ci[1], src);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t me = 64u * (uint32_t)h + (uint32_t)lane;
+            rank[h] += (df < ex[h] || (df == ex[h] && (idf < ci[h] || (idf == ci[h] && f < me)))) ? 1u : 0u;
+        }
     }
-    const bool mine = (uint32_t)lane < Lp;
-    const bool real = mine && ci != NONE;
-    float T = (mine && rank == k - 1) ? ex : INFINITY;
+    bool mine[2], real[2];
+    float T = INFINITY;
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        mine[h] = (uint32_t)(64 * h + lane) < Lp;
+        real[h] = mine[h] && ci[h] != NONE;
+        T = (mine[h] && rank[h] == k - 1) ? ex[h] : T;
+        cnt += (uint32_t)__popcll(__ballot(real[h] && rank[h] < k));
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
         T = fminf(T, __shfl_xor(T, off));
-    const uint32_t cnt = (uint32_t)__popcll(__ballot(real && rank < k));
     const float Bx = lower_bound_exact(B, M.xn[q], M.eps_coef, M.shrink, M.rmax);
     const bool certified = (cnt < k) ? !(B < INFINITY) : (T < Bx);
     if (!certified) {
@@ -988,11 +1009,13 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
         return;
     }
     const size_t orow = (size_t)jb.out_row + ql;
-    if (mine && rank < k) {
-        M.out_ids[orow * k + rank] = real ? ci - jb.id_base : NONE;
-        if (M.out_dist)
-            M.out_dist[orow * k + rank] = real ? ex : INFINITY;
-    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (mine[h] && rank[h] < k) {
+            M.out_ids[orow * k + rank[h]] = real[h] ? ci[h] - jb.id_base : NONE;
+            if (M.out_dist)
+                M.out_dist[orow * k + rank[h]] = real[h] ? ex[h] : INFINITY;
+        }
     if (lane == 0 && M.out_size)
         M.out_size[orow] = (int32_t)cnt;
 }
@@ -1357,6 +1380,171 @@ __global__ __launch_bounds__(MERGE_Q) void ung_pack_kernel(PackParams K)
         row[1 + j] = local_src;
 }
 
+// ---------------------------------------------------------------------------
+// large-group graph: the FastGrnnd prune (tagore_graph_builder.cu:1463-1568, kernels
+// build_sampled_reverse_kernel :141-163 and fast_grnnd_prune_kernel :279-387) over the
+// resident exact kNN lists of ung_hip_group_knn.  Rows are local ids.
+// ---------------------------------------------------------------------------
+struct PruneParams {
+    const float *X;
+    uint32_t d;
+    const Job *jobs;
+    uint32_t n_jobs;
+    const uint32_t *ids;  // [rows x list_k] local ids, by (dist, id)
+    const float *dist;
+    const int32_t *size;
+    uint32_t list_k;
+    uint32_t forward_cap, reverse_cap, final_degree;
+    float alpha;
+    uint64_t rows;
+    uint32_t *rev_cnt;    // [rows + 1]: reverse counts, then (scanned) offsets
+    uint32_t *rev_fill;   // [rows] fill positions
+    uint32_t *rev_src;    // [total] source local ids
+    float *rev_dist;
+    uint32_t *graph;      // [rows x (final_degree + 1)]
+};
+
+// Job (group) of a result row: the last job whose first row is <= r.
+__device__ __forceinline__ uint32_t job_of_row(const Job *__restrict__ jobs, uint32_t n_jobs, uint32_t r)
+{
+    uint32_t lo = 0, hi = n_jobs - 1;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].out_row <= r)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+// Reverse edges: source row r adds itself to the list of each of its first forward_cap
+// candidates (counting pass, then, after a scan, the filling pass; the order inside a
+// list is fixed later by sorting).
+template <bool FILL>
+__global__ __launch_bounds__(256) void ung_reverse_kernel(PruneParams K)
+{
+    for (uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; r < K.rows;
+         r += (uint64_t)gridDim.x * blockDim.x) {
+        const Job jb = K.jobs[job_of_row(K.jobs, K.n_jobs, (uint32_t)r)];
+        const uint32_t src = (uint32_t)r - jb.out_row;
+        const uint32_t cnt = min((uint32_t)K.size[r], K.forward_cap);
+        for (uint32_t t = 0; t < cnt; ++t) {
+            const uint32_t dst = jb.out_row + K.ids[r * K.list_k + t];
+            if constexpr (!FILL) {
+                atomicAdd(&K.rev_cnt[dst], 1u);
+            } else {
+                const uint32_t at = K.rev_cnt[dst] + atomicAdd(&K.rev_fill[dst], 1u);
+                K.rev_src[at] = src;
+                K.rev_dist[at] = K.dist[r * K.list_k + t]; // d(src, dst) == d(dst, src) bit for bit
+            }
+        }
+    }
+}
+
+// (dist, id) ascending sort of one value per lane over the wave.
+__device__ __forceinline__ void wave_sort64(float &d, uint32_t &id, int lane)
+{
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const float od = __shfl_xor(d, j);
+            const uint32_t oi = __shfl_xor(id, j);
+            const bool up = (lane & k) == 0;
+            const bool lower = (lane & j) == 0;
+            const bool take = (lower == up) ? cand_less(od, oi, d, id) : cand_less(d, id, od, oi);
+            d = take ? od : d;
+            id = take ? oi : id;
+        }
+}
+
+// One wave (block) per row: forward candidates + the reverse_cap nearest reverse edges,
+// merged by (dist, id) without duplicates, then the greedy alpha scan.
+__global__ __launch_bounds__(64) void ung_prune_kernel(PruneParams K)
+{
+    __shared__ float cd[128];
+    __shared__ uint32_t ci[128];
+    __shared__ float rd[32];
+    __shared__ uint32_t ri[32];
+    __shared__ uint32_t kept[64];
+    __shared__ uint32_t ncand;
+    const int lane = threadIdx.x;
+    const uint64_t r = blockIdx.x;
+    if (r >= K.rows)
+        return;
+    const Job jb = K.jobs[job_of_row(K.jobs, K.n_jobs, (uint32_t)r)];
+    const uint32_t s = (uint32_t)r - jb.out_row;
+    const uint32_t cnt_f = min((uint32_t)K.size[r], K.forward_cap);
+    // the reverse_cap nearest reverse edges: 32 best kept in lanes 0..31 while chunks of
+    // 32 pass through lanes 32..63
+    const uint32_t r0 = K.rev_cnt[r], r1 = K.rev_cnt[r + 1];
+    float bd = INFINITY;
+    uint32_t bi = NONE;
+    for (uint32_t c0 = r0; c0 < r1; c0 += 32) {
+        if (lane >= 32) {
+            const uint32_t at = c0 + (uint32_t)(lane - 32);
+            bd = at < r1 ? K.rev_dist[at] : INFINITY;
+            bi = at < r1 ? K.rev_src[at] : NONE;
+        }
+        wave_sort64(bd, bi, lane);
+    }
+    const uint32_t cnt_r = min(K.reverse_cap, r1 - r0);
+    if ((uint32_t)lane < cnt_r) {
+        rd[lane] = bd;
+        ri[lane] = bi;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        const float *fdp = K.dist + r * K.list_k;
+        const uint32_t *fip = K.ids + r * K.list_k;
+        uint32_t i = 0, j = 0, nc = 0;
+        while (i < cnt_f || j < cnt_r) {
+            const bool take_f = j == cnt_r || (i < cnt_f && !cand_less(rd[j], ri[j], fdp[i], fip[i]));
+            const float dv = take_f ? fdp[i] : rd[j];
+            const uint32_t iv = take_f ? fip[i] : ri[j];
+            i += take_f ? 1u : 0u;
+            j += take_f ? 0u : 1u;
+            if (nc > 0 && ci[nc - 1] == iv)
+                continue; // the same id twice carries the same distance: adjacent
+            cd[nc] = dv;
+            ci[nc] = iv;
+            ++nc;
+        }
+        ncand = nc;
+    }
+    __syncthreads();
+    const uint32_t nc = ncand;
+    const float *__restrict__ X = K.X + (size_t)jb.q_begin * K.d;
+    const int g = lane >> 3, sub = lane & 7;
+    uint32_t na = 0;
+    for (uint32_t c = 0; c < nc && na < K.final_degree; ++c) {
+        const uint32_t t = ci[c];
+        const float dc = cd[c];
+        if (t == s)
+            continue;
+        bool reject = false;
+        for (uint32_t p0 = 0; p0 < na && !reject; p0 += 8) {
+            const uint32_t p = p0 + (uint32_t)g;
+            const bool valid = p < na;
+            const uint32_t piv = valid ? kept[p] : t;
+            const float dij = l2_ref_8lane(X + (size_t)piv * K.d, X + (size_t)t * K.d, K.d, sub);
+            reject = __ballot(valid && sub == 0 && K.alpha * dij < dc) != 0;
+        }
+        if (!reject) {
+            if (lane == 0)
+                kept[na] = t;
+            ++na;
+            __syncthreads();
+        }
+    }
+    uint32_t *row = K.graph + r * (K.final_degree + 1);
+    if (lane == 0)
+        row[0] = na;
+    for (uint32_t j = (uint32_t)lane; j < K.final_degree; j += 64)
+        row[1 + j] = j < na ? kept[j] : s;
+}
+
 // MFMA fragment layout probe: D = A(32x2) * B(2x32) for a known A, B.
 __global__ void ung_mfma_probe_kernel(float *out)
 {
@@ -1495,6 +1683,10 @@ struct ung_hip_ctx {
     DevBuf<MergeItem> gmitems;
     uint32_t group_list_k = 0;
     DevBuf<uint32_t> graph;
+    // large-group prune: reverse-edge counts/offsets, fill positions, lists, scan scratch
+    DevBuf<uint32_t> rv_cnt, rv_fill, rv_src;
+    DevBuf<float> rv_dist;
+    DevBuf<unsigned char> rv_tmp;
     // additional edges: group ranges, LNG rows, point groups, reached flags, result rows
     DevBuf<uint32_t> a_gb, a_op, a_oi, a_pg, a_reached, a_ids;
     DevBuf<int32_t> a_size;
@@ -1556,12 +1748,12 @@ void add_items_for_job(Plan &pl, uint32_t job_index)
     }
 }
 
-// Entries per partial row: the k results plus a margin, at most one wave's lanes
+// Entries per partial row: the k results plus a margin, at most two per merge lane
 // and at most the 4 queues' entries.
 uint32_t pick_lp(uint32_t k, int lt)
 {
     const uint32_t margin = std::max<uint32_t>(4u, k / 4);
-    return std::min<uint32_t>(std::min<uint32_t>(64u, 4u * (uint32_t)lt), k + margin);
+    return std::min<uint32_t>(std::min<uint32_t>(128u, 4u * (uint32_t)lt), k + margin);
 }
 
 // Queue length: k <= LT lets the 4 queues of a query share thresholds.
@@ -1931,8 +2123,8 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
     uint64_t row = 0;
     for (uint32_t g = 0; g < n_groups; ++g) {
         const uint32_t n = grp_size[g];
-        if (n == 0 || n > 65536 || (uint64_t)grp_begin[g] + n > ctx->N) {
-            set_error("ung_hip_group_knn: group %u (begin %u, size %u) invalid for N=%llu (need 1<=n<=65536)", g,
+        if (n == 0 || (uint64_t)grp_begin[g] + n > ctx->N) {
+            set_error("ung_hip_group_knn: group %u (begin %u, size %u) invalid for N=%llu (need n>=1)", g,
                       grp_begin[g], n, (unsigned long long)ctx->N);
             return UNG_HIP_EINVAL;
         }
@@ -1944,7 +2136,9 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         pl.seg_start.push_back(grp_begin[g]);
         pl.seg_vend.push_back(n);
         jb.n_cand = n;
-        jb.split_v = split_size(n);
+        // a group with many query blocks keeps its candidates whole: the blocks already
+        // spread it over the chip, and splits would multiply its partial rows
+        jb.split_v = (n + BQ - 1) / BQ >= 256 ? n : split_size(n);
         jb.n_split = (n + jb.split_v - 1) / jb.split_v;
         jb.part_base = (uint32_t)pl.part_rows;
         jb.out_row = (uint32_t)row;
@@ -2363,6 +2557,11 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     ctx->gjobs.release();
     ctx->gmitems.release();
     ctx->graph.release();
+    ctx->rv_cnt.release();
+    ctx->rv_fill.release();
+    ctx->rv_src.release();
+    ctx->rv_dist.release();
+    ctx->rv_tmp.release();
     ctx->a_gb.release();
     ctx->a_op.release();
     ctx->a_oi.release();
@@ -2570,6 +2769,99 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
         st->kernel_ms += kms;
         st->d2h_ms += ms_since(t1);
         st->wall_ms += ms_since(t0);
+    }
+    return UNG_HIP_OK;
+}
+
+int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t reverse_cap, uint32_t final_degree,
+                              float alpha, uint32_t *out_graph, uint32_t *entry_points, ung_hip_stats *st)
+{
+    clear_error();
+    if (!ctx || !ctx->group.valid) {
+        set_error("ung_hip_prune_group_graph: run ung_hip_group_knn(_device) first");
+        return UNG_HIP_ESTATE;
+    }
+    const uint32_t list_k = ctx->group_list_k;
+    if (!out_graph || final_degree == 0 || final_degree > 64 || reverse_cap > 32 || forward_cap == 0 ||
+        forward_cap > list_k || !(alpha >= 0.0f)) {
+        set_error("ung_hip_prune_group_graph: need out_graph, 1<=final_degree<=64, reverse_cap<=32, "
+                  "1<=forward_cap<=%u (the kNN list length), alpha>=0", list_k);
+        return UNG_HIP_EINVAL;
+    }
+    int rc;
+    if ((rc = set_device(ctx)))
+        return rc;
+    const auto t0 = clk::now();
+    const uint32_t stride = final_degree + 1;
+    const uint64_t rows = ctx->group.rows;
+    const uint32_t n_jobs = (uint32_t)ctx->group_jobs.size();
+    if (rows == 0 || n_jobs == 0)
+        return UNG_HIP_OK;
+    if (rows >= (1ull << 31)) {
+        set_error("ung_hip_prune_group_graph: %llu rows (at most 2^31-1)", (unsigned long long)rows);
+        return UNG_HIP_EINVAL;
+    }
+    if ((rc = ctx->graph.ensure(rows * stride)) || (rc = ctx->rv_cnt.ensure(rows + 1)) ||
+        (rc = ctx->rv_fill.ensure(rows)))
+        return rc;
+    PruneParams K{};
+    K.X = ctx->X;
+    K.d = ctx->d;
+    K.jobs = ctx->gjobs.p;
+    K.n_jobs = n_jobs;
+    K.ids = ctx->group.ids.p;
+    K.dist = ctx->group.dist.p;
+    K.size = ctx->group.size.p;
+    K.list_k = list_k;
+    K.forward_cap = forward_cap;
+    K.reverse_cap = reverse_cap;
+    K.final_degree = final_degree;
+    K.alpha = alpha;
+    K.rows = rows;
+    K.rev_cnt = ctx->rv_cnt.p;
+    K.rev_fill = ctx->rv_fill.p;
+    K.graph = ctx->graph.p;
+    HIPCHECK(hipEventRecord(ctx->ev[6], ctx->stream));
+    const unsigned zb = (unsigned)std::min<uint64_t>((rows + 256) / 256, 65535);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(zb), dim3(256), 0, ctx->stream, ctx->rv_cnt.p, (uint32_t)(rows + 1));
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(zb), dim3(256), 0, ctx->stream, ctx->rv_fill.p, (uint32_t)rows);
+    HIPCHECK(hipGetLastError());
+    const unsigned rb = (unsigned)std::min<uint64_t>((rows + 255) / 256, 16384);
+    hipLaunchKernelGGL(ung_reverse_kernel<false>, dim3(rb), dim3(256), 0, ctx->stream, K);
+    HIPCHECK(hipGetLastError());
+    // counts -> offsets (exclusive scan over rows + 1 entries, in place)
+    size_t tmp_bytes = 0;
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, ctx->rv_cnt.p, ctx->rv_cnt.p, (int)(rows + 1),
+                                              ctx->stream));
+    if ((rc = ctx->rv_tmp.ensure(tmp_bytes + 1)))
+        return rc;
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(ctx->rv_tmp.p, tmp_bytes, ctx->rv_cnt.p, ctx->rv_cnt.p, (int)(rows + 1),
+                                              ctx->stream));
+    uint32_t total = 0;
+    HIPCHECK(hipMemcpyAsync(&total, ctx->rv_cnt.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    if ((rc = ctx->rv_src.ensure((uint64_t)total + 1)) || (rc = ctx->rv_dist.ensure((uint64_t)total + 1)))
+        return rc;
+    K.rev_src = ctx->rv_src.p;
+    K.rev_dist = ctx->rv_dist.p;
+    hipLaunchKernelGGL(ung_reverse_kernel<true>, dim3(rb), dim3(256), 0, ctx->stream, K);
+    HIPCHECK(hipGetLastError());
+    hipLaunchKernelGGL(ung_prune_kernel, dim3((unsigned)rows), dim3(64), 0, ctx->stream, K);
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipEventRecord(ctx->ev[7], ctx->stream));
+    const auto t1 = clk::now();
+    HIPCHECK(hipMemcpyAsync(out_graph, ctx->graph.p, rows * stride * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
+    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    // FastGrnnd's entry point is the group's first point (ep_dev cleared, :2036)
+    if (entry_points)
+        std::memset(entry_points, 0, n_jobs * sizeof(uint32_t));
+    if (st) {
+        float kms = 0;
+        HIPCHECK(hipEventElapsedTime(&kms, ctx->ev[6], ctx->ev[7]));
+        st->kernel_ms += kms;
+        st->d2h_ms += ms_since(t1);
+        st->wall_ms += ms_since(t0);
+        st->rows += rows;
     }
     return UNG_HIP_OK;
 }

@@ -168,6 +168,18 @@ class HipContext:
                                                 C.byref(st)))
         return graph, entries[:n_groups], st.as_dict()
 
+    def prune_group_graph(self, rows: int, n_groups: int, forward_cap: int, reverse_cap: int,
+                          final_degree: int, alpha: float):
+        """FastGrnnd-style prune of the last group_knn(_device) lists (ung_hip_prune_group_graph):
+        rows [rows x (final_degree+1)] = [count, local ids, padding], entry points, stats."""
+        stride = final_degree + 1
+        graph = np.empty((rows, stride), np.uint32)
+        entries = np.empty(max(n_groups, 1), np.uint32)
+        st = Stats()
+        check(self.lib.ung_hip_prune_group_graph(self.h, forward_cap, reverse_cap, final_degree, alpha, ptr(graph),
+                                                 ptr(entries), C.byref(st)))
+        return graph, entries[:n_groups], st.as_dict()
+
     def synchronize(self):
         check(self.lib.ung_hip_synchronize(self.h))
 
@@ -313,13 +325,15 @@ class UngBuildStage:
     include/config.h:51), ``max_degree`` (include/config.h:41; 32 in the target
     configs), ``tagore_k`` (UNG_TAGORE_K, default 64, src/ung_build_config.cpp:341),
     ``tagore_min_group_size`` / ``exact_max_nx`` (mid-group range 128..4096,
-    src/ung_build_config.cpp:339, src/ung_build_settings.cpp:246-252)."""
+    src/ung_build_config.cpp:339, src/ung_build_settings.cpp:246-252), ``alpha`` (the
+    prune factor, include/config.h)."""
 
     def __init__(self, num_cross_edges: int = 6, max_degree: int = 32, tagore_k: int = 64,
                  tagore_min_group_size: int = 128, exact_max_nx: int = 4096, device: int = 0,
-                 num_threads: int = 0):
+                 num_threads: int = 0, alpha: float = 1.2):
         self.num_cross_edges = int(num_cross_edges)
         self.max_degree = int(max_degree)
+        self.alpha = float(alpha)
         self.tagore_k = int(tagore_k)
         self.tagore_min_group_size = int(tagore_min_group_size)
         self.exact_max_nx = int(exact_max_nx)
@@ -448,6 +462,42 @@ class UngBuildStage:
         gids = np.nonzero((sizes > complete_threshold) & (sizes >= self.tagore_min_group_size) &
                           (sizes <= self.exact_max_nx))[0] + 1
         return gids.astype(np.uint32)
+
+    def large_groups(self):
+        """Groups above the exact batch that the reference gives to the FastGrnnd batch
+        (partition_tagore_groups + build_tagore_batch_artifacts: n > exact_max_nx;
+        src/uni_nav_graph_group_graph.cpp:617-738)."""
+        sizes = np.diff(self.group_begin.astype(np.int64))[1:]
+        complete_threshold = max(self.max_degree, 64)
+        gids = np.nonzero((sizes > complete_threshold) & (sizes >= self.tagore_min_group_size) &
+                          (sizes > self.exact_max_nx))[0] + 1
+        return gids.astype(np.uint32)
+
+    def build_large_group_graph(self, group_ids=None, forward_cap: int | None = None,
+                                reverse_cap: int | None = None) -> TagoreBatchBuildResult:
+        """Graph rows of the large groups: exact candidate lists (list_k = min(64, tagore_k-1))
+        and the FastGrnnd prune (ung_hip_prune_group_graph), with the defaults of
+        make_fast_grnnd_prune_config (src/tagore_cuda_config.cpp:45-68)."""
+        if group_ids is None:
+            group_ids = self.large_groups()
+        group_ids = np.asarray(group_ids, np.int64)
+        begins = self.group_begin[group_ids].astype(np.uint32)
+        sizes = (self.group_begin[group_ids + 1] - self.group_begin[group_ids]).astype(np.uint32)
+        fd = self.max_degree
+        tk = self.tagore_k if self.tagore_k > fd else fd + 1
+        list_k = min(64, tk - 1)
+        if forward_cap is None:
+            forward_cap = min(tk - 1, max(fd, 2 * fd), list_k)
+        if reverse_cap is None:
+            reverse_cap = min(32, max(1, fd))
+        st = self.ctx.group_knn_device(begins, sizes, list_k)
+        graph, entries, st2 = self.ctx.prune_group_graph(int(sizes.astype(np.int64).sum()), len(group_ids),
+                                                         forward_cap, reverse_cap, fd, self.alpha)
+        offsets = np.zeros(len(group_ids) + 1, np.uint32)
+        offsets[1:] = np.cumsum(sizes)
+        st["prune_kernel_ms"] = st2["kernel_ms"]
+        st["prune_wall_ms"] = st2["wall_ms"]
+        return TagoreBatchBuildResult(graph, offsets, fd + 1, entries, None, None, st)
 
     def build_fast_exact_batch(self, group_ids=None, list_k: int | None = None,
                                head_keep: int | None = None, anchor_tail: int = 1,

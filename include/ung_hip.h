@@ -145,7 +145,7 @@ int ung_hip_additional_edges(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group
  * Rows are packed group after group (row offset of group g = sum of earlier sizes,
  * the packed_offsets of TagoreBatchBuildResult, include/tagore_graph_builder.h:80-88).
  * Output (host memory): out_ids [sum n x list_k] local ids, out_dist (nullable).
- * 1 <= list_k <= 64; 2 <= n <= 65536 per group. */
+ * 1 <= list_k <= 64; n >= 1 per group. */
 int ung_hip_group_knn(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
                       const uint32_t *grp_size, uint32_t list_k, uint32_t *out_ids,
                       float *out_dist, ung_hip_stats *st);
@@ -174,6 +174,29 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
                              uint32_t head_keep, uint32_t anchor_tail, uint32_t anchor_slots,
                              uint32_t bidir_anchor, uint32_t *out_graph, uint32_t *entry_points,
                              ung_hip_stats *st);
+
+/* Graph of groups too large for the exact batch (n above exact_max_nx), from the last
+ * ung_hip_group_knn(_device) result (exact lists, list_k = min(64, tagore_k - 1)).  Replaces
+ * build_tagore_vamana_cuda_batch's FastGrnnd path (src/tagore_graph_builder.cu:1777-2159):
+ * its candidate graph comes from the un-vendored NN-descent (here: the exact lists), and its
+ * prune launch_fast_grnnd_prune_impl (:1463-1568) is restated:
+ *  - reverse edges (build_sampled_reverse_kernel :141-163): source s is a reverse candidate
+ *    of each of its first forward_cap list entries; of those, each point keeps the
+ *    reverse_cap nearest by (dist, source id) (the reference keeps the first reverse_cap
+ *    arrivals of an atomic counter, which depend on the run);
+ *  - fast_grnnd_prune_kernel (:279-387): forward (first forward_cap entries) and reverse
+ *    candidates by (dist, id) without duplicates, then a greedy scan keeps a candidate unless
+ *    alpha * d(kept, candidate) < d(point, candidate) for a kept one, up to final_degree
+ *    (distances in the reference's fp32 summation order; the reference prunes on fp16
+ *    copies).
+ * Defaults of make_fast_grnnd_prune_config (src/tagore_cuda_config.cpp:45-68) for tagore_k =
+ * 64, final_degree = 32: forward_cap = 63, reverse_cap = 32.
+ * out_graph (host): [sum n x (final_degree + 1)]: [count, local ids..., padded with the
+ * point's own id]; entry_points (nullable): [n_groups], 0 (the reference clears ep_dev,
+ * :2036).  1 <= final_degree <= 64, reverse_cap <= 32, 1 <= forward_cap <= list_k. */
+int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t reverse_cap,
+                              uint32_t final_degree, float alpha, uint32_t *out_graph,
+                              uint32_t *entry_points, ung_hip_stats *st);
 
 /* Synchronise the context's stream (for callers timing the device variants). */
 int ung_hip_synchronize(ung_hip_ctx *ctx);

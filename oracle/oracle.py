@@ -124,6 +124,9 @@ class Oracle:
         L.ungo_additional_edges.argtypes = _ADDL_ARGS
         L.ungo_assemble_graph.restype = C.c_int64
         L.ungo_assemble_graph.argtypes = _ASM_ARGS
+        L.ungo_large_group_graph.restype = None
+        L.ungo_large_group_graph.argtypes = [_f32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                             C.c_uint32, C.c_uint32, C.c_float, _u32p]
         L.ungo_pack_anchor_row.restype = None
         L.ungo_pack_anchor_row.argtypes = [_u32p, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                            C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
@@ -205,6 +208,15 @@ class Oracle:
         dists = np.zeros((n, K), np.float32)
         self.lib.ungo_intra_exact(X, X.shape[1], begin, n, K, ids, dists, nthreads)
         return ids, dists
+
+    def large_group_graph(self, X, begin, n, knn_k=63, forward_cap=63, reverse_cap=32, final_degree=32,
+                          alpha=1.2):
+        """Rows [n x (final_degree+1)] of ungo_large_group_graph (count, local ids, padding)."""
+        X = _f32(X)
+        rows = np.zeros((n, final_degree + 1), np.uint32)
+        self.lib.ungo_large_group_graph(X, X.shape[1], begin, n, knn_k, forward_cap, reverse_cap, final_degree,
+                                        alpha, rows)
+        return rows
 
     def additional_edges(self, X, group_begin, out_ptr, out_idx, cross_ids, num_cross):
         return _additional_edges(self.lib.ungo_additional_edges, X, group_begin, out_ptr, out_idx,

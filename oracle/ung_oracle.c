@@ -580,3 +580,104 @@ void ungo_pack_anchor_row(const uint32_t *top_idx, uint32_t cand_degree, uint32_
     for (uint32_t j = out_degree; j + 1 < graph_stride; ++j)
         row[1 + j] = local_src;
 }
+
+/* ---- large-group graph: exact candidate lists + the FastGrnnd prune ----
+ * tagore_graph_builder.cu:1777-2159 (batch driver: candidate graph, then
+ * launch_fast_grnnd_prune_impl :1463-1568), build_sampled_reverse_kernel :141-163,
+ * fast_grnnd_prune_kernel :279-387, configuration tagore_cuda_config.cpp:45-68. */
+
+typedef struct {
+    float d;
+    uint32_t id;
+} dist_id;
+
+static int cmp_dist_id(const void *x, const void *y)
+{
+    const dist_id *a = (const dist_id *)x, *b = (const dist_id *)y;
+    if (cand_less(a->d, a->id, b->d, b->id))
+        return -1;
+    if (cand_less(b->d, b->id, a->d, a->id))
+        return 1;
+    return 0;
+}
+
+void ungo_large_group_graph(const float *X, uint32_t dim, uint32_t begin, uint32_t n, uint32_t knn_k,
+                            uint32_t forward_cap, uint32_t reverse_cap, uint32_t final_degree, float alpha,
+                            uint32_t *rows)
+{
+    const uint32_t stride = final_degree + 1;
+    uint32_t *ids = (uint32_t *)malloc((size_t)n * knn_k * sizeof(uint32_t));
+    float *ds = (float *)malloc((size_t)n * knn_k * sizeof(float));
+    ungo_intra_exact(X, dim, begin, n, knn_k, ids, ds, 0);
+    const uint32_t deg = n > 0 ? (knn_k < n - 1 ? knn_k : n - 1) : 0;
+    const uint32_t fwd = deg < forward_cap ? deg : forward_cap;
+    /* reverse lists: every source whose first `fwd` candidates hold the point */
+    uint32_t *rcnt = (uint32_t *)calloc((size_t)n + 1, sizeof(uint32_t));
+    for (uint32_t s = 0; s < n; ++s)
+        for (uint32_t j = 0; j < fwd; ++j)
+            rcnt[ids[(size_t)s * knn_k + j] + 1]++;
+    for (uint32_t i = 0; i < n; ++i)
+        rcnt[i + 1] += rcnt[i];
+    dist_id *rev = (dist_id *)malloc(((size_t)rcnt[n] + 1) * sizeof(dist_id));
+    uint32_t *pos = (uint32_t *)malloc(((size_t)n + 1) * sizeof(uint32_t));
+    memcpy(pos, rcnt, ((size_t)n + 1) * sizeof(uint32_t));
+    for (uint32_t s = 0; s < n; ++s)
+        for (uint32_t j = 0; j < fwd; ++j) {
+            const uint32_t t = ids[(size_t)s * knn_k + j];
+            rev[pos[t]].d = ds[(size_t)s * knn_k + j]; /* dist(s, t) == dist(t, s) bit for bit */
+            rev[pos[t]].id = s;
+            pos[t]++;
+        }
+#pragma omp parallel
+    {
+        dist_id *cand = (dist_id *)malloc(((size_t)fwd + reverse_cap + 1) * sizeof(dist_id));
+        uint32_t *acc = (uint32_t *)malloc(((size_t)final_degree + 1) * sizeof(uint32_t));
+#pragma omp for schedule(dynamic, 16)
+        for (int64_t si = 0; si < (int64_t)n; ++si) {
+            const uint32_t s = (uint32_t)si;
+            uint32_t nc = 0;
+            for (uint32_t j = 0; j < fwd; ++j) {
+                cand[nc].d = ds[(size_t)s * knn_k + j];
+                cand[nc].id = ids[(size_t)s * knn_k + j];
+                nc++;
+            }
+            /* sampled reverse edges: the reverse_cap nearest by (dist, source id) */
+            const uint32_t r0 = rcnt[s], r1 = rcnt[s + 1];
+            qsort(rev + r0, r1 - r0, sizeof(dist_id), cmp_dist_id);
+            for (uint32_t j = r0; j < r1 && j - r0 < reverse_cap; ++j)
+                cand[nc++] = rev[j];
+            qsort(cand, nc, sizeof(dist_id), cmp_dist_id);
+            /* equal ids carry equal distances, so duplicates are adjacent */
+            uint32_t w = 0;
+            for (uint32_t j = 0; j < nc; ++j)
+                if (w == 0 || cand[j].id != cand[w - 1].id)
+                    cand[w++] = cand[j];
+            nc = w;
+            uint32_t na = 0;
+            for (uint32_t j = 0; j < nc && na < final_degree; ++j) {
+                const uint32_t t = cand[j].id;
+                if (t == s)
+                    continue;
+                int reject = 0;
+                for (uint32_t p = 0; p < na && !reject; ++p) {
+                    const float dij = ungo_l2(X + ((size_t)begin + acc[p]) * dim, X + ((size_t)begin + t) * dim, dim);
+                    if (alpha * dij < cand[j].d)
+                        reject = 1;
+                }
+                if (!reject)
+                    acc[na++] = t;
+            }
+            uint32_t *row = rows + (size_t)s * stride;
+            row[0] = na;
+            for (uint32_t j = 0; j < final_degree; ++j)
+                row[1 + j] = j < na ? acc[j] : s;
+        }
+        free(cand);
+        free(acc);
+    }
+    free(ids);
+    free(ds);
+    free(rcnt);
+    free(rev);
+    free(pos);
+}

@@ -133,6 +133,27 @@ void ungo_pack_anchor_row(const uint32_t *top_idx, uint32_t cand_degree, uint32_
                           uint32_t anchor_tail, uint32_t anchor_slots, uint32_t bidir_anchor,
                           uint32_t graph_stride, uint32_t *row);
 
+/* Graph of a large group (n above the exact batch), restating the FastGrnnd batch path
+ * (tagore_graph_builder.cu:1777-2159) with exact candidate lists in place of its
+ * un-vendored NN-descent, and the in-tree prune:
+ *  1. candidates: the exact top-knn_k of every point by (dist, local id)
+ *     (special_blocks.cpp:70-111 order);
+ *  2. build_sampled_reverse_kernel (:141-163): source s joins the reverse list of every
+ *     point among its first forward_cap candidates; the reference keeps the first
+ *     reverse_cap arrivals of an atomic counter (run-dependent), here the reverse_cap
+ *     nearest by (dist, source id);
+ *  3. fast_grnnd_prune_kernel (:279-387): forward (first forward_cap) + reverse
+ *     candidates sorted by (dist, id), duplicates dropped, then a greedy scan keeps a
+ *     candidate unless alpha * d(kept, candidate) < d(point, candidate) for a kept one,
+ *     up to final_degree; distances in fp32 (ungo_l2) where the reference uses fp16.
+ * rows: [n x (final_degree+1)]: row[0] = kept count, row[1..] kept local ids, padded
+ * with the point's own local id (:385-387).  Parity with the reference itself is
+ * unpinned (NN-descent source absent, reverse sampling run-dependent); this function
+ * is the specification the device path is checked against. */
+void ungo_large_group_graph(const float *X, uint32_t dim, uint32_t begin, uint32_t n, uint32_t knn_k,
+                            uint32_t forward_cap, uint32_t reverse_cap, uint32_t final_degree, float alpha,
+                            uint32_t *rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -405,3 +405,98 @@ def test_pack_anchor_invariants(oracle):
         if tail == 1:
             assert len(set(body)) == len(body)
         assert (row[1 + od:] == src).all()
+
+
+# ---- large-group graph (ungo_large_group_graph) -----------------------------------------
+# Integer coordinates keep every squared distance exact in fp32 and float64, so the
+# candidate lists, reverse lists and the prune are checked against an exact distance
+# matrix computed by numpy, with many equal distances (ties broken by id).
+
+def _lg_problem(rng, n, dim, lo=-3, hi=4):
+    X = rng.integers(lo, hi, size=(n + 5, dim)).astype(np.float32)
+    X[7] = X[9]  # an exact duplicate: distance 0
+    D = ((X[5:, None, :].astype(np.float64) - X[None, 5:, :]) ** 2).sum(-1)
+    return X, D
+
+
+def _lg_candidates(D, s, knn_k, forward_cap, reverse_cap):
+    """Sorted, duplicate-free candidate list of point s from the exact matrix D."""
+    n = D.shape[0]
+
+    def fwd(p):
+        o = [j for j in np.lexsort((np.arange(n), D[p])) if j != p]
+        return o[:min(knn_k, n - 1, forward_cap)]
+
+    f = fwd(s)
+    rev = [p for p in range(n) if p != s and s in fwd(p)]
+    rev = sorted(rev, key=lambda p: (D[s, p], p))[:reverse_cap]
+    c = sorted(set(f) | set(rev), key=lambda t: (D[s, t], t))
+    return f, rev, c
+
+
+@pytest.mark.parametrize("n,dim,knn_k,fcap,rcap,fd,alpha,seed",
+                         [(60, 3, 10, 10, 4, 6, 1.2, 1), (80, 5, 12, 8, 5, 7, 1.0, 2),
+                          (50, 2, 20, 20, 8, 12, 1.5, 3)])
+def test_large_group_graph_characterisation(oracle, n, dim, knn_k, fcap, rcap, fd, alpha, seed):
+    """The kept list is the unique greedy result: a subsequence of the sorted candidates,
+    no kept t has an earlier kept p with alpha*d(p,t) < d(s,t), every skipped candidate
+    before the stop point has one, and the row is padded with s."""
+    rng = np.random.default_rng(seed)
+    X, D = _lg_problem(rng, n, dim)
+    rows = oracle.large_group_graph(X, 5, n, knn_k, fcap, rcap, fd, alpha)
+    a = np.float32(alpha)
+    for s in range(n):
+        _, _, cand = _lg_candidates(D, s, knn_k, fcap, rcap)
+        na = int(rows[s, 0])
+        kept = [int(v) for v in rows[s, 1:1 + na]]
+        assert all(int(v) == s for v in rows[s, 1 + na:])
+        assert na <= fd
+        pos = [cand.index(t) for t in kept]  # raises if not a candidate
+        assert pos == sorted(pos)
+        stop = pos[-1] if na == fd else len(cand) - 1
+        for i, t in enumerate(kept):
+            assert not any(a * np.float32(D[p, t]) < np.float32(D[s, t]) for p in kept[:i])
+        for j in range(stop + 1):
+            t = cand[j]
+            if t in kept or t == s:
+                continue
+            earlier = [p for p in kept if cand.index(p) < j]
+            assert any(a * np.float32(D[p, t]) < np.float32(D[s, t]) for p in earlier), (s, t)
+
+
+def test_large_group_graph_no_prune_closed_form(oracle):
+    """alpha so large that nothing is rejected: the row is the first final_degree of the
+    sorted candidate union (forward list + nearest reverse edges)."""
+    rng = np.random.default_rng(7)
+    n, dim, knn_k, fcap, rcap, fd = 70, 4, 9, 9, 6, 14
+    X, D = _lg_problem(rng, n, dim, -20, 21)
+    X[7] = X[8] + 1  # no exact duplicates here: alpha * 0 < d would reject a copy of a kept point
+    D = ((X[5:, None, :].astype(np.float64) - X[None, 5:, :]) ** 2).sum(-1)
+    assert (D + np.eye(n) > 0).all()
+    rows = oracle.large_group_graph(X, 5, n, knn_k, fcap, rcap, fd, 1e30)
+    for s in range(n):
+        f, rev, cand = _lg_candidates(D, s, knn_k, fcap, rcap)
+        want = cand[:fd]
+        assert rows[s, 0] == len(want)
+        assert list(rows[s, 1:1 + len(want)]) == want
+    # alpha = 0 keeps nothing but the first candidate: 0 * d < d(s,t) for every d(s,t) > 0
+    rows0 = oracle.large_group_graph(X, 5, n, knn_k, fcap, rcap, fd, 0.0)
+    for s in range(n):
+        _, _, cand = _lg_candidates(D, s, knn_k, fcap, rcap)
+        kept = list(rows0[s, 1:1 + rows0[s, 0]])
+        assert kept[0] == cand[0]
+        assert all(D[s, t] == 0 for t in kept[1:])  # only distance-0 candidates survive
+
+
+def test_large_group_graph_reverse_rule(oracle):
+    """A point that is in everyone's forward list (the centre of a star) keeps only the
+    reverse_cap nearest reverse edges: with no forward edges (forward_cap=1 to its single
+    nearest) and no pruning, its row is its forward entry plus those reverse edges."""
+    dim = 2
+    pts = [[0, 0]] + [[r, 0] for r in range(1, 30)]
+    X = np.array([[100, 100]] * 5 + pts, np.float32)
+    rows = oracle.large_group_graph(X, 5, len(pts), 1, 1, 4, 10, 1e30)
+    # every point's nearest is its left neighbour (ties by id): 1->0, 2->1, ...; point 0's
+    # nearest is 1; reverse lists: point r has source r+1 only, point 0 has source 1
+    assert list(rows[0, :3]) == [1, 1, 0]  # forward 1 = reverse 1: one candidate
+    assert list(rows[5, :4]) == [2, 4, 6, 5]
