@@ -194,6 +194,40 @@ class Backend {
         return r;
     }
 
+    // The FastGrnnd batch of build_tagore_vamana_cuda_batch (src/tagore_graph_builder.cu:
+    // 1777-2159) for groups above the exact batch: exact candidate lists of length
+    // min(64, k-1) (in place of NN-descent) and the FastGrnnd prune with the caps of
+    // make_fast_grnnd_prune_config (src/tagore_cuda_config.cpp:45-68).  Rows [count, local
+    // ids...] with stride final_degree+1, entry points 0.
+    ExactBatchResult build_large_group_batch(const std::vector<std::pair<uint32_t, uint32_t>> &groups /*begin, n*/,
+                                             uint32_t k, uint32_t final_degree, float alpha)
+    {
+        ExactBatchResult r;
+        if (k <= final_degree)
+            k = final_degree + 1;
+        std::vector<uint32_t> begin(groups.size()), size(groups.size());
+        r.packed_offsets.assign(groups.size() + 1, 0);
+        for (size_t i = 0; i < groups.size(); ++i) {
+            begin[i] = groups[i].first;
+            size[i] = groups[i].second;
+            r.packed_offsets[i + 1] = r.packed_offsets[i] + size[i];
+        }
+        const uint64_t rows = r.packed_offsets.back();
+        const uint32_t list_k = std::min<uint32_t>(64, k - 1);
+        const uint32_t forward_cap = std::min(list_k, std::max(final_degree, 2 * final_degree));
+        const uint32_t reverse_cap = std::min<uint32_t>(32, std::max<uint32_t>(1, final_degree));
+        r.list_k = list_k;
+        throw_if(ung_hip_group_knn_device(ctx_, (uint32_t)groups.size(), begin.data(), size.data(), list_k, &r.stats),
+                 "build_large_group_batch (kNN)");
+        r.packed_graph_stride = final_degree + 1;
+        r.packed_graph.assign(rows * r.packed_graph_stride, 0);
+        r.entry_points.assign(groups.size(), 0);
+        throw_if(ung_hip_prune_group_graph(ctx_, forward_cap, reverse_cap, final_degree, alpha, r.packed_graph.data(),
+                                           r.entry_points.data(), &r.stats),
+                 "build_large_group_batch (prune)");
+        return r;
+    }
+
     const ung_hip_stats &last_stats() const { return last_; }
     ung_hip_ctx *handle() const { return ctx_; }
 
