@@ -967,13 +967,29 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
         B = fminf(bmin, a_next);
     }
 
-    // exact re-score, one lane per candidate and slot
+    // exact re-score: 8 lanes per candidate (one per accumulator of the reference's
+    // summation), 8 candidates per pass; candidate t's value goes to lane t % 64, slot t / 64
     const float *qv = M.X + (size_t)q * M.d;
     float ex[2] = {INFINITY, INFINITY};
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-        if (ci[h] != NONE)
-            ex[h] = l2_ref_lane(qv, M.X + (size_t)ci[h] * M.d, M.d);
+    {
+        const int g = lane >> 3, sub = lane & 7;
+        const uint32_t npass = (Lp + 7u) / 8u;
+        for (uint32_t p = 0; p < npass; ++p) {
+            const uint32_t t = 8u * p + (uint32_t)g;
+            const int src = (int)(t & 63u);
+            const uint32_t c = t < 64u ? __shfl(ci[0], src) : __shfl(ci[1], src);
+            const bool ok = t < Lp && c != NONE;
+            const float v = l2_ref_8lane(qv, M.X + (size_t)(ok ? c : q) * M.d, M.d, sub);
+            const float got = __shfl(v, 8 * (lane & 7)); // candidate 8p + (lane % 8)
+            const uint32_t pl = p & 7u;
+            if ((uint32_t)g == pl) {
+                if (p < 8u)
+                    ex[0] = ci[0] != NONE ? got : INFINITY;
+                else
+                    ex[1] = ci[1] != NONE ? got : INFINITY;
+            }
+        }
+    }
     // rank under (exact, id, position)
     uint32_t rank[2] = {0u, 0u};
     for (uint32_t f = 0; f < Lp; ++f) {
