@@ -10,9 +10,11 @@ A step = the whole device job with the base set already resident in HBM:
 host work-list packing + descriptor upload + MFMA select + merge + exact
 fallback for the cross edges, the additional edges of the groups whose
 out-groups no cross edge reaches (edge lists returned to the host, as the
-reference's materialized lists), then the intra-group kNN.  Cross and intra
-results stay in HBM.  value = (P_cross + P_intra) / step time (distance
-evaluations/s, algorithmic pairs only).
+reference's materialized lists), and the intra-group kNN -- by default started on
+the library's second stream with the cross edges (ung_hip_cross_intra_begin) and
+collected after the additional edges (ung_hip_intra_end); --sequential runs the three
+one after the other.  Cross and intra results stay in HBM.  value = (P_cross +
+P_intra) / step time (distance evaluations/s, algorithmic pairs only).
 
 Prints ONE JSON line.
 """
@@ -123,6 +125,9 @@ def main():
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--n", type=int, default=0, help="override point count (smaller runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sequential", action="store_true",
+                    help="cross edges, additional edges and the mid groups' kNN one after the other "
+                         "(default: the kNN overlapped on the second stream)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="end with a 1 GiB device-to-device copy (counter calibration for --pmc runs)")
@@ -159,12 +164,16 @@ def main():
     log(f"resident upload {up['h2d_ms']:.1f} ms ({st.base.nbytes / up['h2d_ms'] / 1e6:.1f} GB/s incl. PCIe)")
 
     def step():
-        s1 = ctx.cross_topk_device(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross)
+        if args.sequential:
+            s1 = ctx.cross_topk_device(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross)
+        else:  # the mid groups' kNN runs on the second stream beside the cross tail
+            s1 = ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross, begins, sizes,
+                                       cfg.k_intra)
         t0 = time.perf_counter()
         _, ef, _, s3 = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross)
         s3["wall_ms"] = (time.perf_counter() - t0) * 1e3
         s3["edges"] = int(ef.size)
-        s2 = ctx.group_knn_device(begins, sizes, cfg.k_intra)
+        s2 = ctx.group_knn_device(begins, sizes, cfg.k_intra) if args.sequential else ctx.intra_end()
         return s1, s2, s3
 
     for _ in range(args.warmup):
@@ -228,7 +237,8 @@ def main():
                                f"{cfg.m_min}-{cfg.m_max} labels Zipf({cfg.zipf_s}); cross k={cfg.k_cross} + "
                                f"intra exact K={cfg.k_intra} for 128<=n<=4096",
                    "groups": st.num_groups, "lng_edges": int(len(st.out_idx)), "mid_groups": int(len(gids)),
-                   "P_cross": int(p_cross), "P_intra": int(p_intra)},
+                   "P_cross": int(p_cross), "P_intra": int(p_intra),
+                   "intra_overlapped": not args.sequential},
         "roofline": roofline,
         "breakdown": {
             "cross_wall_ms": round(avg(cross_stats, "wall_ms"), 3),

@@ -77,6 +77,8 @@ SIGNATURES = {
     "ung_hip_download_group": (_int, [_vp, _vp, _vp, _vp]),
     "ung_hip_pack_anchor_rows": (_int, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     "ung_hip_prune_group_graph": (_int, [_vp, _u32, _u32, _u32, C.c_float, _vp, _vp, _vp]),
+    "ung_hip_cross_intra_begin": (_int, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _vp, _vp, _u32, _vp]),
+    "ung_hip_intra_end": (_int, [_vp, _vp]),
     "ung_hip_synchronize": (_int, [_vp]),
     "ung_hip_selftest_mfma": (_int, [_vp, C.POINTER(_dbl)]),
     "ung_divide_groups": (_int, [_u64, _vp, _vp, _vp, _vp, _vp, C.POINTER(_u32)]),

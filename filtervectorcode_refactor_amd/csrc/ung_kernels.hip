@@ -1664,9 +1664,45 @@ struct ResultBufs {
 
 } // namespace
 
+namespace {
+// Work lists, partial rows, flags and timing events of one planned call, with the stream
+// it runs on.  A context has two, so a group kNN call can run on the second stream while
+// the cross-edge call and the additional edges use the first.
+struct Workspace {
+    hipStream_t stream = nullptr;
+    hipEvent_t ev[4] = {};
+    DevBuf<Job> jobs;
+    DevBuf<Item> items;
+    DevBuf<MergeItem> mitems;
+    DevBuf<uint32_t> seg_start, seg_vend;
+    DevBuf<uint32_t> part_ids;
+    DevBuf<float> part_dist;
+    DevBuf<float> part_bound;
+    DevBuf<uint32_t> flag_count; // [0]: rows flagged for the rescan, [1]: select item counter
+    DevBuf<uint2> flagged;
+    DevBuf<uint32_t> fb_ids; // rescan range results
+    DevBuf<float> fb_dist;
+    void release()
+    {
+        jobs.release();
+        items.release();
+        mitems.release();
+        seg_start.release();
+        seg_vend.release();
+        part_ids.release();
+        part_dist.release();
+        part_bound.release();
+        flag_count.release();
+        flagged.release();
+        fb_ids.release();
+        fb_dist.release();
+    }
+};
+} // namespace
+
 struct ung_hip_ctx {
     int device = 0;
-    hipStream_t stream = nullptr;
+    hipStream_t stream = nullptr; // the first workspace's stream
     hipEvent_t ev[8] = {};
     // resident base set
     float *X = nullptr;
@@ -1677,18 +1713,15 @@ struct ung_hip_ctx {
     uint64_t N = 0;
     uint32_t d = 0;
     double rmax = 0.0;
-    // work lists / scratch
-    DevBuf<Job> jobs;
-    DevBuf<Item> items;
-    DevBuf<MergeItem> mitems;
-    DevBuf<uint32_t> seg_start, seg_vend;
-    DevBuf<uint32_t> part_ids;
-    DevBuf<float> part_dist;
-    DevBuf<float> part_bound;
-    DevBuf<uint32_t> flag_count;
-    DevBuf<uint2> flagged;
-    DevBuf<uint32_t> fb_ids; // fallback range results
-    DevBuf<float> fb_dist;
+    // work lists / scratch: [0] cross edges, additional edges and synchronous group calls,
+    // [1] the group call started by ung_hip_cross_intra_begin
+    Workspace ws[2];
+    // a group call in flight on ws[1] (ung_hip_cross_intra_begin .. ung_hip_intra_end)
+    bool intra_pending = false;
+    Plan intra_plan;
+    uint32_t intra_list_k = 0;
+    ung_hip_stats intra_stats{};
+    std::chrono::steady_clock::time_point intra_t0;
     // results
     ResultBufs cross;
     ResultBufs group;
@@ -1783,7 +1816,7 @@ int pick_lt(uint32_t k)
 }
 
 template <int LT>
-int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, bool excl)
+int launch_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P, uint32_t n_items, bool excl)
 {
     // 32-bit buffer offsets need a split base set below 4 GiB
     const uint64_t x_bytes = (uint64_t)ctx->N * ctx->dp * sizeof(uint32_t);
@@ -1797,18 +1830,18 @@ int launch_select_t(ung_hip_ctx *ctx, const SelectParams &P, uint32_t n_items, b
         const uint32_t n = std::min(max_grid, n_items - off);
         Q.n_items = n;
         if (off > 0) { // the counter was zeroed for the first chunk by the caller
-            hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ctx->stream, P.item_ctr, 1u);
+            hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, stream, P.item_ctr, 1u);
             HIPCHECK(hipGetLastError());
         }
         const dim3 g(n), b(NTHREADS);
         if (mode == LOAD_BUF32 && excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true>), g, b, 0, stream, Q);
         else if (mode == LOAD_BUF32)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false>), g, b, 0, stream, Q);
         else if (excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true>), g, b, 0, stream, Q);
         else
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false>), g, b, 0, ctx->stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false>), g, b, 0, stream, Q);
         HIPCHECK(hipGetLastError());
     }
     return UNG_HIP_OK;
@@ -1835,20 +1868,23 @@ double eps_coef_for(uint32_t d)
     return (1.75 * (double)d + 112.0) * std::ldexp(1.0, -24);
 }
 
-// Runs a planned job list; results into `res` (rows x k), rows of res already
-// initialised by the caller when some rows have no job.
-int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st)
+// Runs a planned job list on workspace `ws`; results into `res` (rows x k), rows of res
+// already initialised by the caller when some rows have no job.  plan_launch uploads the
+// work lists and enqueues the select and merge kernels; plan_finish reads the flagged-row
+// count back, rescans those rows and collects the statistics.
+int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st,
+                hipEvent_t start_after = nullptr)
 {
     int rc;
     const int lt = pick_lt(k);
     const uint32_t lp = pick_lp(k, lt);
     const auto t_h2d = clk::now();
-    if ((rc = ctx->jobs.ensure(pl.jobs.size())) || (rc = ctx->items.ensure(pl.items.size())) ||
-        (rc = ctx->mitems.ensure(pl.mitems.size())) || (rc = ctx->seg_start.ensure(pl.seg_start.size())) ||
-        (rc = ctx->seg_vend.ensure(pl.seg_vend.size())) ||
-        (rc = ctx->part_ids.ensure(pl.part_rows * lp)) || (rc = ctx->part_dist.ensure(pl.part_rows * lp)) ||
-        (rc = ctx->part_bound.ensure(pl.part_rows)) || (rc = ctx->flag_count.ensure(2)) ||
-        (rc = ctx->flagged.ensure(std::max<uint64_t>(pl.rows, 1))))
+    if ((rc = ws.jobs.ensure(pl.jobs.size())) || (rc = ws.items.ensure(pl.items.size())) ||
+        (rc = ws.mitems.ensure(pl.mitems.size())) || (rc = ws.seg_start.ensure(pl.seg_start.size())) ||
+        (rc = ws.seg_vend.ensure(pl.seg_vend.size())) ||
+        (rc = ws.part_ids.ensure(pl.part_rows * lp)) || (rc = ws.part_dist.ensure(pl.part_rows * lp)) ||
+        (rc = ws.part_bound.ensure(pl.part_rows)) || (rc = ws.flag_count.ensure(2)) ||
+        (rc = ws.flagged.ensure(std::max<uint64_t>(pl.rows, 1))))
         return rc;
     // select items in order of decreasing cost (candidate tiles); the stable sort keeps
     // the query blocks of one split next to each other
@@ -1857,61 +1893,64 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
         return (a.v_end - a.v_begin + BC - 1) / BC > (b.v_end - b.v_begin + BC - 1) / BC;
     });
     if (!pl.jobs.empty()) {
-        HIPCHECK(hipMemcpyAsync(ctx->jobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->items.p, order.data(), order.size() * sizeof(Item), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->mitems.p, pl.mitems.data(), pl.mitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->seg_start.p, pl.seg_start.data(), pl.seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->seg_vend.p, pl.seg_vend.data(), pl.seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ws.jobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.items.p, order.data(), order.size() * sizeof(Item), hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.mitems.p, pl.mitems.data(), pl.mitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.seg_start.p, pl.seg_start.data(), pl.seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.seg_vend.p, pl.seg_vend.data(), pl.seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ws.stream));
     }
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    HIPCHECK(hipStreamSynchronize(ws.stream));
     if (st)
         st->h2d_ms += ms_since(t_h2d);
     if (pl.jobs.empty())
         return UNG_HIP_OK;
 
+    // kernels of this plan start after `start_after` (another stream's event), if given
+    if (start_after)
+        HIPCHECK(hipStreamWaitEvent(ws.stream, start_after, 0));
     // flag_count[0]: rows flagged for the fallback, [1]: select item counter
-    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ctx->stream, ctx->flag_count.p, 2u);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ws.stream, ws.flag_count.p, 2u);
     HIPCHECK(hipGetLastError());
-    HIPCHECK(hipEventRecord(ctx->ev[0], ctx->stream));
+    HIPCHECK(hipEventRecord(ws.ev[0], ws.stream));
 
     SelectParams P{};
     P.xs = ctx->XS;
     P.xn = ctx->xn;
     P.dp = ctx->dp;
     P.k = k;
-    P.jobs = ctx->jobs.p;
-    P.items = ctx->items.p;
-    P.seg_start = ctx->seg_start.p;
-    P.seg_vend = ctx->seg_vend.p;
-    P.part_ids = ctx->part_ids.p;
-    P.part_dist = ctx->part_dist.p;
-    P.part_bound = ctx->part_bound.p;
+    P.jobs = ws.jobs.p;
+    P.items = ws.items.p;
+    P.seg_start = ws.seg_start.p;
+    P.seg_vend = ws.seg_vend.p;
+    P.part_ids = ws.part_ids.p;
+    P.part_dist = ws.part_dist.p;
+    P.part_bound = ws.part_bound.p;
     P.eps_coef = eps_coef_for(ctx->d) * ctx->eps_scale;
     P.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
     P.rmax = ctx->rmax;
-    P.item_ctr = ctx->flag_count.p + 1;
+    P.item_ctr = ws.flag_count.p + 1;
     P.lp = lp;
     const uint32_t n_items = (uint32_t)pl.items.size();
     const bool excl = (pl.jobs[0].flags & 1u) != 0; // one kind of job per plan
     if (lt == 8)
-        rc = launch_select_t<8>(ctx, P, n_items, excl);
+        rc = launch_select_t<8>(ctx, ws.stream, P, n_items, excl);
     else if (lt == 16)
-        rc = launch_select_t<16>(ctx, P, n_items, excl);
+        rc = launch_select_t<16>(ctx, ws.stream, P, n_items, excl);
     else
-        rc = launch_select_t<32>(ctx, P, n_items, excl);
+        rc = launch_select_t<32>(ctx, ws.stream, P, n_items, excl);
     if (rc)
         return rc;
-    HIPCHECK(hipEventRecord(ctx->ev[1], ctx->stream));
+    HIPCHECK(hipEventRecord(ws.ev[1], ws.stream));
 
     MergeParams M{};
     M.X = ctx->X;
     M.xn = ctx->xn;
     M.d = ctx->d;
-    M.jobs = ctx->jobs.p;
-    M.mitems = ctx->mitems.p;
-    M.part_ids = ctx->part_ids.p;
-    M.part_dist = ctx->part_dist.p;
-    M.part_bound = ctx->part_bound.p;
+    M.jobs = ws.jobs.p;
+    M.mitems = ws.mitems.p;
+    M.part_ids = ws.part_ids.p;
+    M.part_dist = ws.part_dist.p;
+    M.part_bound = ws.part_bound.p;
     M.lp = lp;
     M.k = k;
     M.eps_coef = P.eps_coef;
@@ -1920,20 +1959,28 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
     M.out_ids = res.ids.p;
     M.out_dist = res.dist.p;
     M.out_size = res.size.p;
-    M.flag_count = ctx->flag_count.p;
-    M.flagged = ctx->flagged.p;
+    M.flag_count = ws.flag_count.p;
+    M.flagged = ws.flagged.p;
     const uint32_t n_m = (uint32_t)pl.mitems.size();
     for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
         MergeParams Mc = M;
         Mc.mitems = M.mitems + off;
         const uint32_t n = std::min<uint32_t>(1u << 30, n_m - off);
-        hipLaunchKernelGGL(ung_merge_kernel, dim3(n), dim3(64 * MERGE_ROWS), 0, ctx->stream, Mc);
+        hipLaunchKernelGGL(ung_merge_kernel, dim3(n), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
         HIPCHECK(hipGetLastError());
     }
-    HIPCHECK(hipEventRecord(ctx->ev[2], ctx->stream));
+    HIPCHECK(hipEventRecord(ws.ev[2], ws.stream));
+    return UNG_HIP_OK;
+}
+
+int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st)
+{
+    int rc;
+    if (pl.jobs.empty())
+        return UNG_HIP_OK;
     uint32_t nflag = 0;
-    HIPCHECK(hipMemcpyAsync(&nflag, ctx->flag_count.p, sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    HIPCHECK(hipMemcpyAsync(&nflag, ws.flag_count.p, sizeof(uint32_t), hipMemcpyDeviceToHost, ws.stream));
+    HIPCHECK(hipStreamSynchronize(ws.stream));
     if (nflag > 0) {
         // a flagged row's union is cut into ranges of >= FALLBACK_RANGE candidates
         uint64_t max_cand = 0;
@@ -1945,38 +1992,38 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
         F.X = ctx->X;
         F.d = ctx->d;
         F.k = k;
-        F.jobs = ctx->jobs.p;
-        F.seg_start = ctx->seg_start.p;
-        F.seg_vend = ctx->seg_vend.p;
-        F.flag_count = ctx->flag_count.p;
-        F.flagged = ctx->flagged.p;
+        F.jobs = ws.jobs.p;
+        F.seg_start = ws.seg_start.p;
+        F.seg_vend = ws.seg_vend.p;
+        F.flag_count = ws.flag_count.p;
+        F.flagged = ws.flagged.p;
         F.splits = S;
         F.out_ids = res.ids.p;
         F.out_dist = res.dist.p;
         F.out_size = res.size.p;
         if (S > 1) {
-            if ((rc = ctx->fb_ids.ensure((uint64_t)nflag * S * k)) || (rc = ctx->fb_dist.ensure((uint64_t)nflag * S * k)))
+            if ((rc = ws.fb_ids.ensure((uint64_t)nflag * S * k)) || (rc = ws.fb_dist.ensure((uint64_t)nflag * S * k)))
                 return rc;
-            F.part_ids = ctx->fb_ids.p;
-            F.part_dist = ctx->fb_dist.p;
+            F.part_ids = ws.fb_ids.p;
+            F.part_dist = ws.fb_dist.p;
         }
         const uint64_t items = (uint64_t)nflag * S;
         hipLaunchKernelGGL(ung_fallback_kernel, dim3((unsigned)std::min<uint64_t>(items, 1u << 20)), dim3(64), 0,
-                           ctx->stream, F);
+                           ws.stream, F);
         HIPCHECK(hipGetLastError());
         if (S > 1) {
             hipLaunchKernelGGL(ung_fallback_merge_kernel, dim3(std::min<uint32_t>(nflag, 8192u)), dim3(64), 0,
-                               ctx->stream, F);
+                               ws.stream, F);
             HIPCHECK(hipGetLastError());
         }
     }
-    HIPCHECK(hipEventRecord(ctx->ev[3], ctx->stream));
-    HIPCHECK(hipEventSynchronize(ctx->ev[3]));
+    HIPCHECK(hipEventRecord(ws.ev[3], ws.stream));
+    HIPCHECK(hipEventSynchronize(ws.ev[3]));
     if (st) {
         float a = 0, b = 0, c = 0;
-        HIPCHECK(hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[1]));
-        HIPCHECK(hipEventElapsedTime(&b, ctx->ev[1], ctx->ev[2]));
-        HIPCHECK(hipEventElapsedTime(&c, ctx->ev[2], ctx->ev[3]));
+        HIPCHECK(hipEventElapsedTime(&a, ws.ev[0], ws.ev[1]));
+        HIPCHECK(hipEventElapsedTime(&b, ws.ev[1], ws.ev[2]));
+        HIPCHECK(hipEventElapsedTime(&c, ws.ev[2], ws.ev[3]));
         st->select_ms += a;
         st->merge_ms += b;
         st->fallback_ms += c;
@@ -1993,6 +2040,14 @@ int run_plan(ung_hip_ctx *ctx, const Plan &pl, uint32_t k, ResultBufs &res, ung_
         st->select_launches += 1;
     }
     return UNG_HIP_OK;
+}
+
+int run_plan(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st)
+{
+    int rc;
+    if ((rc = plan_launch(ctx, ws, pl, k, res, st)))
+        return rc;
+    return plan_finish(ctx, ws, pl, k, res, st);
 }
 
 int check_ready(ung_hip_ctx *ctx)
@@ -2079,6 +2134,31 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
     return UNG_HIP_OK;
 }
 
+int build_group_plan(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin, const uint32_t *grp_size,
+                     uint32_t list_k, Plan &pl);
+int group_prepare_result(ung_hip_ctx *ctx, const Plan &pl, uint32_t list_k);
+int group_complete(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t list_k);
+int check_not_pending(ung_hip_ctx *ctx, const char *who);
+
+// Result rows of a cross call, initialised (padding) on the first workspace's stream.
+int cross_prepare_result(ung_hip_ctx *ctx, uint32_t k)
+{
+    int rc;
+    ResultBufs &res = ctx->cross;
+    res.valid = false;
+    if ((rc = res.ids.ensure(ctx->N * k)) || (rc = res.dist.ensure(ctx->N * k)) || (rc = res.size.ensure(ctx->N)))
+        return rc;
+    res.rows = ctx->N;
+    res.k = k;
+    const uint64_t tot = ctx->N * k;
+    if (tot > 0) {
+        hipLaunchKernelGGL(ung_fill_rows_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, ctx->ws[0].stream,
+                           res.ids.p, res.dist.p, res.size.p, ctx->N, k);
+        HIPCHECK(hipGetLastError());
+    }
+    return UNG_HIP_OK;
+}
+
 int cross_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
                  const uint32_t *out_idx, uint32_t k, ung_hip_stats *st)
 {
@@ -2097,33 +2177,102 @@ int cross_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, cons
         return rc;
     if (st)
         st->plan_ms += ms_since(t0);
-    ResultBufs &res = ctx->cross;
-    res.valid = false;
-    if ((rc = res.ids.ensure(ctx->N * k)) || (rc = res.dist.ensure(ctx->N * k)) || (rc = res.size.ensure(ctx->N)))
+    if ((rc = cross_prepare_result(ctx, k)) || (rc = run_plan(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
         return rc;
-    res.rows = ctx->N;
-    res.k = k;
-    const uint64_t tot = ctx->N * k;
-    if (tot > 0) {
-        hipLaunchKernelGGL(ung_fill_rows_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, ctx->stream,
-                           res.ids.p, res.dist.p, res.size.p, ctx->N, k);
-        HIPCHECK(hipGetLastError());
-    }
-    if ((rc = run_plan(ctx, pl, k, res, st)))
-        return rc;
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
-    res.valid = true;
+    HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
+    ctx->cross.valid = true;
     if (st)
         st->wall_ms += ms_since(t0);
     return UNG_HIP_OK;
 }
 
-int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin, const uint32_t *grp_size,
-                 uint32_t list_k, ung_hip_stats *st)
+// Cross edges on the first workspace and a group kNN call on the second, overlapped: the
+// group call's kernels start when the cross select ends and run beside the cross merge,
+// rescan and whatever the caller does next (additional edges).
+int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
+                      const uint32_t *out_idx, uint32_t k, uint32_t n_groups, const uint32_t *grp_begin,
+                      const uint32_t *grp_size, uint32_t list_k, ung_hip_stats *st)
 {
     int rc;
-    if ((rc = check_ready(ctx)))
+    if ((rc = check_ready(ctx)) || (rc = check_not_pending(ctx, "ung_hip_cross_intra_begin")))
         return rc;
+    if (k < 1 || k > 64) {
+        set_error("k=%u outside 1..64", k);
+        return UNG_HIP_EINVAL;
+    }
+    if ((rc = set_device(ctx)))
+        return rc;
+    const auto t0 = clk::now();
+    Plan pl;
+    if ((rc = build_cross_plan(ctx, G, group_begin, out_ptr, out_idx, pl)))
+        return rc;
+    if (st)
+        st->plan_ms += ms_since(t0);
+    ctx->intra_stats = ung_hip_stats{};
+    ctx->intra_t0 = clk::now();
+    ctx->intra_plan = Plan{};
+    if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, ctx->intra_plan)))
+        return rc;
+    ctx->intra_stats.plan_ms += ms_since(ctx->intra_t0);
+    if ((rc = cross_prepare_result(ctx, k)) || (rc = plan_launch(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
+        return rc;
+    // from here the group call is in flight on the second workspace until intra_end
+    ctx->intra_list_k = list_k;
+    ctx->intra_pending = true;
+    // the group call's kernels start when the cross select ends: they fill the chip while
+    // the cross merge (memory-bound), rescan and the caller's next steps run
+    if ((rc = group_prepare_result(ctx, ctx->intra_plan, list_k)) ||
+        (rc = plan_launch(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats,
+                          ctx->ws[0].ev[1])))
+        return rc;
+    if ((rc = plan_finish(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
+        return rc;
+    HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
+    ctx->cross.valid = true;
+    if (st)
+        st->wall_ms += ms_since(t0);
+    return UNG_HIP_OK;
+}
+
+int intra_end(ung_hip_ctx *ctx, ung_hip_stats *st)
+{
+    int rc;
+    if (!ctx || !ctx->intra_pending) {
+        set_error("ung_hip_intra_end: no group kNN call in flight");
+        return UNG_HIP_ESTATE;
+    }
+    if ((rc = set_device(ctx)))
+        return rc;
+    ctx->intra_pending = false;
+    const uint32_t list_k = ctx->intra_list_k;
+    if ((rc = plan_finish(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats)) ||
+        (rc = group_complete(ctx, ctx->ws[1], ctx->intra_plan, list_k)))
+        return rc;
+    ctx->intra_stats.wall_ms += ms_since(ctx->intra_t0);
+    if (st) {
+        st->wall_ms += ctx->intra_stats.wall_ms;
+        st->plan_ms += ctx->intra_stats.plan_ms;
+        st->h2d_ms += ctx->intra_stats.h2d_ms;
+        st->kernel_ms += ctx->intra_stats.kernel_ms;
+        st->select_ms += ctx->intra_stats.select_ms;
+        st->merge_ms += ctx->intra_stats.merge_ms;
+        st->fallback_ms += ctx->intra_stats.fallback_ms;
+        st->d2h_ms += ctx->intra_stats.d2h_ms;
+        st->pairs += ctx->intra_stats.pairs;
+        st->rows += ctx->intra_stats.rows;
+        st->work_items += ctx->intra_stats.work_items;
+        st->select_launches += ctx->intra_stats.select_launches;
+        st->fallback_rows += ctx->intra_stats.fallback_rows;
+        st->padded_pairs += ctx->intra_stats.padded_pairs;
+        st->select_bytes += ctx->intra_stats.select_bytes;
+    }
+    return UNG_HIP_OK;
+}
+
+// Validated job list of a group kNN call: one job per group, its own range as candidates.
+int build_group_plan(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin, const uint32_t *grp_size,
+                     uint32_t list_k, Plan &pl)
+{
     if (list_k < 1 || list_k > 64) {
         set_error("list_k=%u outside 1..64", list_k);
         return UNG_HIP_EINVAL;
@@ -2132,10 +2281,6 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         set_error("ung_hip_group_knn: null grp_begin/grp_size");
         return UNG_HIP_EINVAL;
     }
-    if ((rc = set_device(ctx)))
-        return rc;
-    const auto t0 = clk::now();
-    Plan pl;
     uint64_t row = 0;
     for (uint32_t g = 0; g < n_groups; ++g) {
         const uint32_t n = grp_size[g];
@@ -2171,29 +2316,71 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         pl.jobs.push_back(jb);
         add_items_for_job(pl, (uint32_t)pl.jobs.size() - 1);
     }
-    if (st)
-        st->plan_ms += ms_since(t0);
+    return UNG_HIP_OK;
+}
+
+int group_prepare_result(ung_hip_ctx *ctx, const Plan &pl, uint32_t list_k)
+{
+    int rc;
     ResultBufs &res = ctx->group;
     res.valid = false;
-    if ((rc = res.ids.ensure(std::max<uint64_t>(row * list_k, 1))) ||
-        (rc = res.dist.ensure(std::max<uint64_t>(row * list_k, 1))) || (rc = res.size.ensure(std::max<uint64_t>(row, 1))))
+    if ((rc = res.ids.ensure(std::max<uint64_t>(pl.rows * list_k, 1))) ||
+        (rc = res.dist.ensure(std::max<uint64_t>(pl.rows * list_k, 1))) ||
+        (rc = res.size.ensure(std::max<uint64_t>(pl.rows, 1))))
         return rc;
-    res.rows = row;
+    res.rows = pl.rows;
     res.k = list_k;
-    if ((rc = run_plan(ctx, pl, list_k, res, st)))
-        return rc;
-    // keep the job table for packing
+    return UNG_HIP_OK;
+}
+
+// Keeps the job table for packing and pruning, marks the lists valid.
+int group_complete(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t list_k)
+{
+    int rc;
     ctx->group_jobs = pl.jobs;
     ctx->group_pitems = pl.pitems;
     ctx->group_list_k = list_k;
     if (!pl.jobs.empty()) {
         if ((rc = ctx->gjobs.ensure(pl.jobs.size())) || (rc = ctx->gmitems.ensure(pl.pitems.size())))
             return rc;
-        HIPCHECK(hipMemcpyAsync(ctx->gjobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->gmitems.p, pl.pitems.data(), pl.pitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->gjobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ctx->gmitems.p, pl.pitems.data(), pl.pitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ws.stream));
     }
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
-    res.valid = true;
+    HIPCHECK(hipStreamSynchronize(ws.stream));
+    ctx->group.valid = true;
+    return UNG_HIP_OK;
+}
+
+int check_not_pending(ung_hip_ctx *ctx, const char *who)
+{
+    if (ctx->intra_pending) {
+        set_error("%s: a group kNN call started by ung_hip_cross_intra_begin is in flight (call ung_hip_intra_end first)",
+                  who);
+        return UNG_HIP_ESTATE;
+    }
+    return UNG_HIP_OK;
+}
+
+int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin, const uint32_t *grp_size,
+                 uint32_t list_k, ung_hip_stats *st)
+{
+    int rc;
+    if ((rc = check_ready(ctx)) || (rc = check_not_pending(ctx, "ung_hip_group_knn")))
+        return rc;
+    if ((rc = set_device(ctx)))
+        return rc;
+    const auto t0 = clk::now();
+    Plan pl;
+    if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, pl)))
+        return rc;
+    if (st)
+        st->plan_ms += ms_since(t0);
+    if ((rc = group_prepare_result(ctx, pl, list_k)))
+        return rc;
+    if ((rc = run_plan(ctx, ctx->ws[0], pl, list_k, ctx->group, st)))
+        return rc;
+    if ((rc = group_complete(ctx, ctx->ws[0], pl, list_k)))
+        return rc;
     if (st)
         st->wall_ms += ms_since(t0);
     return UNG_HIP_OK;
@@ -2323,26 +2510,26 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     std::vector<int32_t> size;
     if (!rows.empty()) {
         const uint64_t R = rows.size();
-        if ((rc = ctx->jobs.ensure(jobs.size())) || (rc = ctx->seg_start.ensure(seg_start.size())) ||
-            (rc = ctx->seg_vend.ensure(seg_vend.size())) || (rc = ctx->flagged.ensure(R)) ||
-            (rc = ctx->flag_count.ensure(2)) || (rc = ctx->a_ids.ensure(R * per_max)) || (rc = ctx->a_size.ensure(R)))
+        if ((rc = ctx->ws[0].jobs.ensure(jobs.size())) || (rc = ctx->ws[0].seg_start.ensure(seg_start.size())) ||
+            (rc = ctx->ws[0].seg_vend.ensure(seg_vend.size())) || (rc = ctx->ws[0].flagged.ensure(R)) ||
+            (rc = ctx->ws[0].flag_count.ensure(2)) || (rc = ctx->a_ids.ensure(R * per_max)) || (rc = ctx->a_size.ensure(R)))
             return rc;
         const uint32_t nrows = (uint32_t)R;
-        HIPCHECK(hipMemcpyAsync(ctx->jobs.p, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->seg_start.p, seg_start.data(), seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->seg_vend.p, seg_vend.data(), seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->flagged.p, rows.data(), R * sizeof(uint2), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->flag_count.p, &nrows, sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->ws[0].jobs.p, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->ws[0].seg_start.p, seg_start.data(), seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->ws[0].seg_vend.p, seg_vend.data(), seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->ws[0].flagged.p, rows.data(), R * sizeof(uint2), hipMemcpyHostToDevice, ctx->stream));
+        HIPCHECK(hipMemcpyAsync(ctx->ws[0].flag_count.p, &nrows, sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
         HIPCHECK(hipEventRecord(ctx->ev[0], ctx->stream));
         FallbackParams F{};
         F.X = ctx->X;
         F.d = ctx->d;
         F.k = per_max;
-        F.jobs = ctx->jobs.p;
-        F.seg_start = ctx->seg_start.p;
-        F.seg_vend = ctx->seg_vend.p;
-        F.flag_count = ctx->flag_count.p;
-        F.flagged = ctx->flagged.p;
+        F.jobs = ctx->ws[0].jobs.p;
+        F.seg_start = ctx->ws[0].seg_start.p;
+        F.seg_vend = ctx->ws[0].seg_vend.p;
+        F.flag_count = ctx->ws[0].flag_count.p;
+        F.flagged = ctx->ws[0].flagged.p;
         F.splits = 1;
         F.out_ids = ctx->a_ids.p;
         F.out_dist = nullptr;
@@ -2423,7 +2610,7 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
         return UNG_HIP_EINVAL;
     }
     int rc;
-    if ((rc = set_device(ctx)))
+    if ((rc = check_not_pending(ctx, "ung_hip_prepare_vectors")) || (rc = set_device(ctx)))
         return rc;
     ung_hip_release_vectors(ctx);
     const auto t0 = clk::now();
@@ -2502,19 +2689,23 @@ int ung_hip_create(int device, ung_hip_ctx **out)
         const double v = std::atof(s);
         ctx->eps_scale = v >= 1.0 ? v : 1.0; // a smaller bound would not be an error bound
     }
-    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-    if (e != hipSuccess) {
-        set_error("hipStreamCreateWithFlags failed: %s", hipGetErrorString(e));
-        delete ctx;
-        return UNG_HIP_EDEVICE;
+    hipError_t e = hipSuccess;
+    for (auto &w : ctx->ws) { // both streams at the default priority
+        e = hipStreamCreateWithFlags(&w.stream, hipStreamNonBlocking);
+        for (auto &ev : w.ev)
+            if (e == hipSuccess)
+                e = hipEventCreate(&ev);
+        if (e != hipSuccess)
+            break;
     }
-    for (auto &ev : ctx->ev) {
-        e = hipEventCreate(&ev);
-        if (e != hipSuccess) {
-            set_error("hipEventCreate failed: %s", hipGetErrorString(e));
-            ung_hip_destroy(ctx);
-            return UNG_HIP_EDEVICE;
-        }
+    ctx->stream = ctx->ws[0].stream;
+    for (auto &ev : ctx->ev)
+        if (e == hipSuccess)
+            e = hipEventCreate(&ev);
+    if (e != hipSuccess) {
+        set_error("stream/event creation failed: %s", hipGetErrorString(e));
+        ung_hip_destroy(ctx);
+        return UNG_HIP_EDEVICE;
     }
     *out = ctx;
     return UNG_HIP_OK;
@@ -2527,6 +2718,9 @@ int ung_hip_release_vectors(ung_hip_ctx *ctx)
         set_error("null context");
         return UNG_HIP_EINVAL;
     }
+    int rc;
+    if ((rc = check_not_pending(ctx, "ung_hip_release_vectors")))
+        return rc;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream)
         (void)hipStreamSynchronize(ctx->stream);
@@ -2555,19 +2749,14 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     clear_error();
     if (!ctx)
         return UNG_HIP_OK;
+    (void)hipSetDevice(ctx->device);
+    for (auto &w : ctx->ws)
+        if (w.stream)
+            (void)hipStreamSynchronize(w.stream);
+    ctx->intra_pending = false;
     ung_hip_release_vectors(ctx);
-    ctx->jobs.release();
-    ctx->items.release();
-    ctx->mitems.release();
-    ctx->seg_start.release();
-    ctx->seg_vend.release();
-    ctx->part_ids.release();
-    ctx->part_dist.release();
-    ctx->part_bound.release();
-    ctx->flag_count.release();
-    ctx->flagged.release();
-    ctx->fb_ids.release();
-    ctx->fb_dist.release();
+    for (auto &w : ctx->ws)
+        w.release();
     ctx->cross.release();
     ctx->group.release();
     ctx->gjobs.release();
@@ -2588,8 +2777,13 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     for (auto &ev : ctx->ev)
         if (ev)
             (void)hipEventDestroy(ev);
-    if (ctx->stream)
-        (void)hipStreamDestroy(ctx->stream);
+    for (auto &w : ctx->ws) {
+        for (auto &ev : w.ev)
+            if (ev)
+                (void)hipEventDestroy(ev);
+        if (w.stream)
+            (void)hipStreamDestroy(w.stream);
+    }
     delete ctx;
     return UNG_HIP_OK;
 }
@@ -2690,6 +2884,20 @@ int ung_hip_group_knn(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_b
     if (st)
         st->wall_ms = ms_since(t0);
     return rc;
+}
+
+int ung_hip_cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
+                              const uint32_t *out_idx, uint32_t k, uint32_t n_groups, const uint32_t *grp_begin,
+                              const uint32_t *grp_size, uint32_t list_k, ung_hip_stats *st)
+{
+    clear_error();
+    return cross_intra_begin(ctx, G, group_begin, out_ptr, out_idx, k, n_groups, grp_begin, grp_size, list_k, st);
+}
+
+int ung_hip_intra_end(ung_hip_ctx *ctx, ung_hip_stats *st)
+{
+    clear_error();
+    return intra_end(ctx, st);
 }
 
 int ung_hip_group_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **dist_dev, uint64_t *rows)

@@ -107,6 +107,26 @@ class HipContext:
                                                  C.byref(st)))
         return st.as_dict()
 
+    def cross_intra_begin(self, group_begin, out_ptr, out_idx, k: int, grp_begin, grp_size, list_k: int) -> dict:
+        """Cross edges (device-resident, complete on return) and a group kNN call left running
+        on the second stream until intra_end (ung_hip_cross_intra_begin)."""
+        group_begin, out_ptr = u32(group_begin), u32(out_ptr)
+        out_idx = u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
+        grp_begin, grp_size = u32(grp_begin), u32(grp_size)
+        G = group_begin.shape[0] - 2
+        st = Stats()
+        check(self.lib.ung_hip_cross_intra_begin(self.h, G, ptr(group_begin), ptr(out_ptr), ptr(out_idx), k,
+                                                 grp_begin.shape[0], ptr(grp_begin) if len(grp_begin) else None,
+                                                 ptr(grp_size) if len(grp_size) else None, list_k, C.byref(st)))
+        self._keep = (grp_begin, grp_size)
+        return st.as_dict()
+
+    def intra_end(self) -> dict:
+        st = Stats()
+        check(self.lib.ung_hip_intra_end(self.h, C.byref(st)))
+        self._keep = None
+        return st.as_dict()
+
     def download_cross(self, N: int, k: int):
         ids = np.empty((N, k), np.uint32)
         dist = np.empty((N, k), np.float32)
@@ -114,6 +134,14 @@ class HipContext:
         st = Stats()
         check(self.lib.ung_hip_download_cross(self.h, ptr(ids), ptr(dist), ptr(size), C.byref(st)))
         return ids, dist, size, st.as_dict()
+
+    def download_group(self, rows: int, list_k: int):
+        """The resident lists of the last group kNN call (ung_hip_download_group)."""
+        ids = np.empty((rows, list_k), np.uint32)
+        dist = np.empty((rows, list_k), np.float32)
+        st = Stats()
+        check(self.lib.ung_hip_download_group(self.h, ptr(ids), ptr(dist), C.byref(st)))
+        return ids, dist, st.as_dict()
 
     def additional_edges(self, group_begin, out_ptr, out_idx, num_cross: int):
         """Additional edges (exact variant) from the resident cross-edge rows of the last

@@ -150,6 +150,22 @@ int ung_hip_group_knn(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_b
                       const uint32_t *grp_size, uint32_t list_k, uint32_t *out_ids,
                       float *out_dist, ung_hip_stats *st);
 
+/* The cross-edge call (ung_hip_cross_topk_device) and a group kNN call
+ * (ung_hip_group_knn_device) overlapped on the context's two streams.  No counterpart in
+ * the reference, which runs build_cross_edges_generate_gpu_optimized
+ * (src/uni_nav_graph_cross_edges.cpp:334-440) and the exact group batch
+ * (src/uni_nav_graph_group_graph.cpp:643-738) one after the other; the results are those
+ * of the two calls.  Returns when the cross-edge rows are complete (as
+ * ung_hip_cross_topk_device); the group call keeps running until ung_hip_intra_end, and
+ * meanwhile calls that read the group lists or replace the base set return
+ * UNG_HIP_ESTATE.  Cross-edge calls and ung_hip_additional_edges may run in between. */
+int ung_hip_cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
+                              const uint32_t *out_ptr, const uint32_t *out_idx, uint32_t k,
+                              uint32_t n_groups, const uint32_t *grp_begin, const uint32_t *grp_size,
+                              uint32_t list_k, ung_hip_stats *st_cross);
+/* Completes the group call of ung_hip_cross_intra_begin (its statistics into st). */
+int ung_hip_intra_end(ung_hip_ctx *ctx, ung_hip_stats *st);
+
 /* Device-resident variant of ung_hip_group_knn (results in context buffers). */
 int ung_hip_group_knn_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
                              const uint32_t *grp_size, uint32_t list_k, ung_hip_stats *st);

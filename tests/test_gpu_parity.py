@@ -292,3 +292,43 @@ def test_pipeline_graph_cfg1(cfg1_stage, oracle, tmp_path):
     st.save_graph(tmp_path / "graph")
     assert (tmp_path / "graph").read_bytes().count(b"\n") == N
     st.close()
+
+
+def test_cross_intra_overlapped_equals_sequential(ctx, oracle):
+    """ung_hip_cross_intra_begin / ung_hip_intra_end (cross edges and the mid groups' kNN
+    on two streams, additional edges in between) give the rows of the sequential calls,
+    and calls that would touch the running group call are refused until it ends."""
+    cfg = D.scaled(D.CONFIGS["cfg2"], 60_000)
+    X, lp, li = D.generate(cfg)
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    ctx.prepare_vectors(st.base)
+    gids = st.mid_groups().astype(np.int64)
+    b = st.group_begin[gids].astype(np.uint32)
+    n = (st.group_begin[gids + 1] - st.group_begin[gids]).astype(np.uint32)
+    _say(f"overlapped cross + intra: {len(gids)} mid groups")
+    c_ids, c_dist, c_size, _ = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+    want_add = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, 6)
+    g_ids, g_dist, _ = ctx.group_knn(b, n, 32)
+    for rep in range(2):
+        ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, 6, b, n, 32)
+        with pytest.raises(F.UngHipError):
+            ctx.prepare_vectors(st.base)
+        with pytest.raises(F.UngHipError):
+            ctx.group_knn(b[:1], n[:1], 32)
+        got_add = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, 6)
+        ids, dist, size, _ = ctx.download_cross(st.base.shape[0], 6)
+        stats = ctx.intra_end()
+        assert stats["rows"] == int(n.sum())
+        with pytest.raises(F.UngHipError):
+            ctx.intra_end()
+        check_ids, check_dist, _ = ctx.download_group(g_ids.shape[0], 32)
+        assert np.array_equal(ids, c_ids) and np.array_equal(dist, c_dist) and np.array_equal(size, c_size)
+        for a, w in zip(got_add[:3], want_add[:3]):
+            assert np.array_equal(a, w)
+        assert np.array_equal(check_ids, g_ids) and np.array_equal(check_dist, g_dist)
+    # the cross rows also equal the oracle's on a sample (the sequential call is pinned elsewhere)
+    pg = st.new_vec_id_to_group_id
+    q = np.arange(0, st.base.shape[0], 97, dtype=np.uint32)
+    res = oracle.cross_exact_points(st.base, st.group_begin, pg, st.out_ptr, st.out_idx, q, 6)
+    _assert_rows_equal(ids[q], dist[q], None, res[0], res[1], None, "overlapped cross sample")
