@@ -129,7 +129,22 @@ __device__ __forceinline__ float l2_ref_8lane(const float *__restrict__ a,
 {
     float acc = 0.0f;
     const uint32_t nb8 = d >> 3;
-    for (uint32_t blk = 0; blk < nb8; ++blk) {
+    uint32_t blk = 0;
+    // 8 blocks of loads in flight before their fused multiply-adds (same order)
+    for (; blk + 8 <= nb8; blk += 8) {
+        float ta[8], tb[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            ta[u] = a[8 * (blk + u) + sub];
+            tb[u] = b[8 * (blk + u) + sub];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float t = ta[u] - tb[u];
+            acc = __builtin_fmaf(t, t, acc);
+        }
+    }
+    for (; blk < nb8; ++blk) {
         const float t = a[8 * blk + sub] - b[8 * blk + sub];
         acc = __builtin_fmaf(t, t, acc);
     }
@@ -164,6 +179,24 @@ __device__ __forceinline__ float l2_ref_lane(const float *__restrict__ a,
     if ((d & 3u) == 0) {
         const float4 *a4 = reinterpret_cast<const float4 *>(a);
         const float4 *b4 = reinterpret_cast<const float4 *>(b);
+        // four 8-float blocks of loads in flight before their fused multiply-adds
+        for (; p + 32 <= d; p += 32) {
+            float4 x[8], y[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                x[u] = a4[(p >> 2) + u];
+                y[u] = b4[(p >> 2) + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u += 2) {
+                const float t[8] = {x[u].x - y[u].x, x[u].y - y[u].y, x[u].z - y[u].z, x[u].w - y[u].w,
+                                    x[u + 1].x - y[u + 1].x, x[u + 1].y - y[u + 1].y, x[u + 1].z - y[u + 1].z,
+                                    x[u + 1].w - y[u + 1].w};
+#pragma unroll
+                for (int l = 0; l < 8; ++l)
+                    acc[l] = __builtin_fmaf(t[l], t[l], acc[l]);
+            }
+        }
         for (; p + 8 <= d; p += 8) {
             const float4 x0 = a4[p >> 2], x1 = a4[(p >> 2) + 1];
             const float4 y0 = b4[p >> 2], y1 = b4[(p >> 2) + 1];
