@@ -523,10 +523,33 @@ __device__ __forceinline__ void best_of_32(float (&d)[32], uint32_t (&id)[32], f
 //                row, candidates through 64-bit row pointers (one add per load).
 enum : int { LOAD_BUF32 = 1, LOAD_WIDE = 2 };
 
-template <int LT, int MODE, bool EXCL>
-__global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
+// Staging area of the NB = 1 layout: each thread's 32 values of its list (row stride 36
+// words spreads the 16-byte stores over the banks).
+struct alignas(16) SelectStage {
+    float v[2 * NTHREADS][36];
+};
+struct NoStage {};
+
+// NB query columns per lane: NB = 2 -- 4 waves, each a 64x64 block (2x2 accumulators),
+// two blocks per CU; NB = 1 -- 8 waves, each a 64x32 block, one block per CU, half the
+// queue registers per lane (long queues at two waves per SIMD).
+template <int NB>
+constexpr int select_threads()
 {
+    return NB == 2 ? NTHREADS : 2 * NTHREADS;
+}
+
+template <int LT, int MODE, bool EXCL, int NB>
+__global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
+{
+    static_assert(NB == 1 || NB == 2, "one or two query columns per lane");
+    constexpr int NTH = select_threads<NB>();
+    constexpr int WN = 4 / NB;         // query waves
+    constexpr int QW = 32 * NB;        // query columns per wave
+    constexpr int RSTEP = NTH / 8;     // loader row step
+    constexpr int LM = BQ / RSTEP;     // rows per thread and panel
     __shared__ SelectSmem sm;
+    __shared__ typename std::conditional<NB == 1, SelectStage, NoStage>::type stage;
     __shared__ uint32_t item_slot;
     const uint32_t logical = take_item(P.item_ctr, &item_slot);
     if (logical >= P.n_items)
@@ -535,7 +558,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     const Job jb = P.jobs[it.job];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int r = lane & 31, h = lane >> 5;
     // block-uniform values loaded with vector loads: readfirstlane keeps the query
     // buffer descriptor of the wide mode in scalar registers
@@ -549,11 +572,14 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     RowCursor cur;
     finish_rowids(sm, 0, start_rowids(sm, 0, cur, P, jb, it.v_begin, it.v_end, tid), tid);
 
-    float ld[2][LT];
-    uint32_t li[2][LT];
-    float tfin[2] = {INFINITY, INFINITY}; // lowest threshold a queue has applied so far
+    float ld[NB][LT];
+    uint32_t li[NB][LT];
+    float tfin[NB]; // lowest threshold a queue has applied so far
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
+        tfin[nb] = INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int j = 0; j < LT; ++j) {
             ld[nb][j] = INFINITY;
@@ -563,30 +589,30 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     // entries already cover the k results
     const bool share = P.k <= (uint32_t)LT;
 
-    // loader mapping: rows lr = (tid>>3) + 32m, columns c4 .. c4+3 of the chunk
+    // loader mapping: rows lr = (tid>>3) + RSTEP*m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
     const int c4 = (tid & 7) * 4;
     [[maybe_unused]] __amdgpu_buffer_rsrc_t qres, xres;
-    [[maybe_unused]] uint32_t xoff[4];
-    [[maybe_unused]] const uint32_t *xrow[4];
+    [[maybe_unused]] uint32_t xoff[LM];
+    [[maybe_unused]] const uint32_t *xrow[LM];
     if constexpr (MODE == LOAD_BUF32) {
         xres = __builtin_amdgcn_make_buffer_rsrc((void *)XS, (short)0, (int)P.x_bytes, 0x00020000);
     } else {
         qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * dp), (short)0, (int)(qcnt * dp * 4u),
                                                  0x00020000);
     }
-    // query rows lr0 + 32m: one vector offset, the 32-row steps as scalar offsets.  Rows
+    // query rows lr0 + RSTEP*m: one vector offset, the row steps as scalar offsets.  Rows
     // past the item's queries (padding columns, whose results are never read) load
     // whatever the buffer holds there, zero beyond its range.
-    const uint32_t qrow_step = 32u * dp * 4u;
+    const uint32_t qrow_step = (uint32_t)RSTEP * dp * 4u;
     const uint32_t qoff = MODE == LOAD_BUF32 ? ((q0 + (uint32_t)lr0) * dp + (uint32_t)c4) * 4u
                                              : ((uint32_t)lr0 * dp + (uint32_t)c4) * 4u;
 
     __syncthreads();
-    float qnv[2];
+    float qnv[NB];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-        qnv[nb] = sm.qn[wn * 64 + nb * 32 + r];
+    for (int nb = 0; nb < NB; ++nb)
+        qnv[nb] = sm.qn[wn * QW + nb * 32 + r];
 
     // One flat software pipeline over (candidate tile, k-chunk) steps: the panels are
     // double-buffered in LDS and each step prefetches the next step's chunk (also
@@ -598,8 +624,8 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 
     auto set_xrows = [&](int slot) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            uint32_t g = sm.rowid[slot][lr0 + 32 * m];
+        for (int m = 0; m < LM; ++m) {
+            uint32_t g = sm.rowid[slot][lr0 + RSTEP * m];
             g = (g == NONE) ? 0u : g; // padding rows load row 0 (their -|x|^2/2 is -inf)
             if constexpr (MODE == LOAD_BUF32)
                 xoff[m] = (g * dp + (uint32_t)c4) * 4u;
@@ -607,10 +633,10 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                 xrow[m] = XS + (size_t)g * dp + c4;
         }
     };
-    float4 rq[4], rx[4]; // raw split words (bf16 pairs), typed for 16-byte moves
+    float4 rq[LM], rx[LM]; // raw split words (bf16 pairs), typed for 16-byte moves
     auto load_chunk = [&](uint32_t kc) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
+        for (int m = 0; m < LM; ++m) {
             if constexpr (MODE == LOAD_BUF32) {
                 rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
@@ -626,7 +652,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     // s = |x|^2/2 - <x,q>  (padding rows: -inf).  Adding the norm term last keeps the
     // running sums at the size of the products, which halves the accumulation error of
     // the certified bound.
-    floatx16 acc[2][2];
+    floatx16 acc[2][NB];
 
     __syncthreads(); // ring slot 0 and qn visible
     set_xrows(0);
@@ -639,9 +665,9 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
         const int buf = (int)(s & 1u);
         const int next_slot = slot == 2 ? 0 : slot + 1;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            sm.u.p.qs[buf][lr0 + 32 * m][c4 >> 2] = rq[m];
-            sm.u.p.xs[buf][lr0 + 32 * m][c4 >> 2] = rx[m];
+        for (int m = 0; m < LM; ++m) {
+            sm.u.p.qs[buf][lr0 + RSTEP * m][c4 >> 2] = rq[m];
+            sm.u.p.xs[buf][lr0 + RSTEP * m][c4 >> 2] = rx[m];
         }
         if (nk == 1 && tile + 1 < ntiles)
             finish_rowids(sm, next_slot,
@@ -671,27 +697,33 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const int ch = 2 * kb + h; // float4 column of the high parts; +4: low parts
-                const bf16x8 ah0 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + r][ch]);
-                const bf16x8 ah1 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + 32 + r][ch]);
-                const bf16x8 bh0 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + r][ch]);
-                const bf16x8 bh1 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + 32 + r][ch]);
-                const bf16x8 al0 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + r][ch + 4]);
-                const bf16x8 al1 = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + 32 + r][ch + 4]);
-                const bf16x8 bl0 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + r][ch + 4]);
-                const bf16x8 bl1 = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * 64 + 32 + r][ch + 4]);
+                bf16x8 ah[2], al[2], bh[NB], bl[NB];
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    ah[mb] = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + 32 * mb + r][ch]);
+                    al[mb] = __builtin_bit_cast(bf16x8, sm.u.p.xs[buf][wm * 64 + 32 * mb + r][ch + 4]);
+                }
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    bh[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * QW + 32 * nb + r][ch]);
+                    bl[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * QW + 32 * nb + r][ch + 4]);
+                }
                 const bool z = FIRST && kb == 0;
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bh0, z ? zero : acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bh1, z ? zero : acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bh0, z ? zero : acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bh1, z ? zero : acc[1][1], 0, 0, 0);
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bl0, acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah0, bl1, acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bl0, acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah1, bl1, acc[1][1], 0, 0, 0);
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al0, bh0, acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al0, bh1, acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al1, bh0, acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al1, bh1, acc[1][1], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[mb], bh[nb], z ? zero : acc[mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[mb], bl[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[mb], bh[nb], acc[mb][nb], 0, 0, 0);
             }
         };
         if (kc == 0)
@@ -706,7 +738,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 
         if (kc + 1 == nk) {
             // epilogue: acc[mb][nb][i] = -s for row tile_row(wm, h, 16*mb + i) and query
-            // col = wn*64+nb*32+r, s = |x|^2/2 - <x,q>; the expansion-form distance is
+            // col = wn*QW+nb*32+r, s = |x|^2/2 - <x,q>; the expansion-form distance is
             // a = fl(2s + |q|^2) = fma(-2, acc, |q|^2) (padding rows: acc = -inf).
             //
             // The four queues of a query (lane halves h, candidate waves wm) share a
@@ -723,13 +755,13 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
 #pragma unroll
-                        for (int nb = 0; nb < 2; ++nb)
+                        for (int nb = 0; nb < NB; ++nb)
                             acc[mb][nb][4 * g4 + e] += nh[e];
                 }
-            float tsh[2], ncth[2];
+            float tsh[NB], ncth[NB];
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const int col = wn * 64 + nb * 32 + r;
+            for (int nb = 0; nb < NB; ++nb) {
+                const int col = wn * QW + nb * 32 + r;
                 const float own = ld[nb][LT - 1];
                 const float partner = __shfl_xor(own, 32);
                 float t = fminf(own, tfin[nb]);
@@ -744,39 +776,52 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
             // branch-free pass: per list a lane mask whose bit (31 - j) marks element j
             // under the pre-filter bound (s < c  <=>  the sign bit of -c - acc; a NaN
             // from -inf - -inf only marks a padding row, which the round rejects)
-            uint32_t pend[2] = {0u, 0u};
+            uint32_t pend[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                pend[nb] = 0u;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
 #pragma unroll
-                    for (int nb = 0; nb < 2; ++nb)
+                    for (int nb = 0; nb < NB; ++nb)
                         pend[nb] = (pend[nb] << 1) | (__float_as_uint(ncth[nb] - acc[mb][nb][i]) >> 31);
             // self exclusion (candidate space = query space): clear the query's own bit
-            uint32_t self_j[2] = {32u, 32u};
+            uint32_t self_j[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                self_j[nb] = 32u;
             if constexpr (EXCL) {
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    const int o = (int)(it.q_off + (uint32_t)(wn * 64 + nb * 32 + r)) -
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int o = (int)(it.q_off + (uint32_t)(wn * QW + nb * 32 + r)) -
                                   (int)(it.v_begin + tile * BC) - (wm * 64 + 4 * h);
                     self_j[nb] = lane_index_of(o);
                     pend[nb] &= self_j[nb] < 32u ? ~(0x80000000u >> self_j[nb]) : 0xFFFFFFFFu;
                 }
             }
-            // Each thread owns the 8 panel slots it fills at the next step (buffer buf^1,
-            // read by no wave before the next barrier): one list's 32 values are staged
-            // there, so a round reads its element with one LDS load instead of a register
-            // select tree.  Slot g holds values 4g..4g+3.
+            // One list's 32 values are staged in LDS, so a round reads its element with one
+            // LDS load instead of a register select tree.  NB = 2: each thread owns the 8
+            // panel slots it fills at the next step (buffer buf^1, read by no wave before
+            // the next barrier), slot g holding values 4g..4g+3; NB = 1: its row of the
+            // staging area.
             float *const pnl = reinterpret_cast<float *>(&sm.u.p);
-            const int own0 = ((buf ^ 1) * BQ + lr0) * LDSW + c4;
+            [[maybe_unused]] const int own0 = ((buf ^ 1) * BQ + lr0) * LDSW + c4;
+            auto staged = [&](uint32_t j) -> float & {
+                if constexpr (NB == 1)
+                    return stage.v[tid][j];
+                else
+                    return pnl[own0 + (int)(j >> 4) * PANEL_X + (int)((j >> 2) & 3u) * ROW32 + (int)(j & 3u)];
+            };
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
+            for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
                 for (int g = 0; g < 8; ++g) {
                     const int mb = g >> 2, g4 = g & 3;
                     const float4 v = make_float4(acc[mb][nb][4 * g4], acc[mb][nb][4 * g4 + 1],
                                                  acc[mb][nb][4 * g4 + 2], acc[mb][nb][4 * g4 + 3]);
-                    *reinterpret_cast<float4 *>(pnl + own0 + mb * PANEL_X + g4 * ROW32) = v;
+                    *reinterpret_cast<float4 *>(&staged(4u * (uint32_t)g)) = v;
                 }
                 uint32_t m = pend[nb];
                 if (tile == 0) {
@@ -817,7 +862,7 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                     const uint32_t j = (uint32_t)__builtin_clz(m | 1u);
                     const bool act = m != 0u;
                     m &= ~(0x80000000u >> j);
-                    const float av = pnl[own0 + (int)(j >> 4) * PANEL_X + (int)((j >> 2) & 3u) * ROW32 + (int)(j & 3u)];
+                    const float av = staged(j);
                     const uint32_t rid = sm.rowid[slot][tile_row(wm, h, j)];
                     float dd = __builtin_fmaf(-2.0f, av, qnv[nb]);
                     dd = (act && dd < fminf(ld[nb][LT - 1], tsh[nb])) ? dd : INFINITY;
@@ -825,13 +870,13 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
                 }
             }
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
+            for (int nb = 0; nb < NB; ++nb) {
                 // publish this wave's threshold of the query for the other wave
                 const float t = fminf(tsh[nb], ld[nb][LT - 1]);
                 tfin[nb] = t;
                 const float pair_t = fminf(t, __shfl_xor(t, 32));
                 if (share && h == 0)
-                    sm.tau[tile & 1][wm][wn * 64 + nb * 32 + r] = pair_t;
+                    sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
             }
             ++tile;
             kc = 0;
@@ -849,11 +894,12 @@ __global__ __launch_bounds__(NTHREADS, (LT <= 8 ? 2 : 1)) void ung_select_kernel
     for (int pass = 0; pass < npass; ++pass) {
         const int rows_here = (int)min(64u, qcnt - (uint32_t)pass * 64u);
         __syncthreads();
-        if (wn == pass) {
+        // the waves whose query columns lie in this pass's 64 queries
+        if ((wn * QW) / 64 == pass) {
             const int lid = wm * 2 + h;
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const int jl = nb * 32 + r;
+            for (int nb = 0; nb < NB; ++nb) {
+                const int jl = (wn * QW) % 64 + nb * 32 + r;
 #pragma unroll
                 for (int j = 0; j < LT; ++j) {
                     sm.u.r.ed[jl][lid * LT + j] = ld[nb][j];
@@ -1866,15 +1912,17 @@ int launch_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P,
             hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, stream, P.item_ctr, 1u);
             HIPCHECK(hipGetLastError());
         }
-        const dim3 g(n), b(NTHREADS);
+        // queues longer than 8 take the one-column-per-lane layout (two waves per SIMD)
+        constexpr int NB = LT <= 8 ? 2 : 1;
+        const dim3 g(n), b(select_threads<NB>());
         if (mode == LOAD_BUF32 && excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true, NB>), g, b, 0, stream, Q);
         else if (mode == LOAD_BUF32)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false, NB>), g, b, 0, stream, Q);
         else if (excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true, NB>), g, b, 0, stream, Q);
         else
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false, NB>), g, b, 0, stream, Q);
         HIPCHECK(hipGetLastError());
     }
     return UNG_HIP_OK;
