@@ -43,10 +43,11 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def read_traffic():
-    """HBM bytes per launch of the cross select kernel, measured offline with
-    rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and calibrated on a copy kernel."""
-    if not os.path.exists(TRAFFIC_FILE):
+def read_traffic(config_name):
+    """HBM bytes per launch of the cross select kernel on cfg2, measured offline with
+    rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and calibrated on a copy kernel; None for
+    other workloads (not measured)."""
+    if config_name != "cfg2" or not os.path.exists(TRAFFIC_FILE):
         return None
     with open(TRAFFIC_FILE) as f:
         for line in f:
@@ -206,7 +207,7 @@ def main():
     flops_cross = 2.0 * d * p_cross
     mfma_flops = 3.0 * 2.0 * dp * p_cross
     alg_bytes = float(cross_stats[-1]["select_bytes"])
-    traffic = read_traffic()
+    traffic = read_traffic(cfg.name) if not args.n else None
     mfma_floor_ms = mfma_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3
     hbm_floor_ms = (traffic if traffic else alg_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
     mfma_tflops = mfma_flops / sel_s / 1e12
