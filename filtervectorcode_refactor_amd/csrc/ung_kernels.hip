@@ -1712,6 +1712,37 @@ struct DevBuf {
     }
 };
 
+// Pinned host memory (hipHostMalloc), grown on demand.
+struct HostBuf {
+    void *p = nullptr;
+    size_t cap = 0; // bytes
+    int ensure(size_t n)
+    {
+        if (n <= cap)
+            return UNG_HIP_OK;
+        if (p)
+            (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        const size_t want = n + n / 4 + 4096;
+        hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            p = nullptr;
+            set_error("hipHostMalloc(%zu bytes) failed: %s", want, hipGetErrorString(e));
+            return UNG_HIP_EDEVICE;
+        }
+        cap = want;
+        return UNG_HIP_OK;
+    }
+    void release()
+    {
+        if (p)
+            (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
 struct Plan {
     std::vector<Job> jobs;
     std::vector<Item> items;
@@ -1761,8 +1792,10 @@ struct Workspace {
     DevBuf<uint2> flagged;
     DevBuf<uint32_t> fb_ids; // rescan range results
     DevBuf<float> fb_dist;
+    HostBuf stage;           // pinned staging of the work-list uploads
     void release()
     {
+        stage.release();
         jobs.release();
         items.release();
         mitems.release();
@@ -1969,18 +2002,37 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
         return rc;
     // select items in order of decreasing cost (candidate tiles); the stable sort keeps
     // the query blocks of one split next to each other
-    std::vector<Item> order(pl.items);
-    std::stable_sort(order.begin(), order.end(), [](const Item &a, const Item &b) {
-        return (a.v_end - a.v_begin + BC - 1) / BC > (b.v_end - b.v_begin + BC - 1) / BC;
-    });
+    // (a counting sort by tile count: stable, linear in the item count)
     if (!pl.jobs.empty()) {
-        HIPCHECK(hipMemcpyAsync(ws.jobs.p, pl.jobs.data(), pl.jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.items.p, order.data(), order.size() * sizeof(Item), hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.mitems.p, pl.mitems.data(), pl.mitems.size() * sizeof(MergeItem), hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.seg_start.p, pl.seg_start.data(), pl.seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.seg_vend.p, pl.seg_vend.data(), pl.seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ws.stream));
+        auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+        const size_t bj = pl.jobs.size() * sizeof(Job), bi = pl.items.size() * sizeof(Item);
+        const size_t bm = pl.mitems.size() * sizeof(MergeItem), bs = pl.seg_start.size() * sizeof(uint32_t);
+        const size_t oj = 0, oi = al(bj), om = oi + al(bi), os = om + al(bm), ov = os + al(bs);
+        if ((rc = ws.stage.ensure(ov + al(bs))))
+            return rc;
+        char *hs = static_cast<char *>(ws.stage.p);
+        std::memcpy(hs + oj, pl.jobs.data(), bj);
+        std::memcpy(hs + om, pl.mitems.data(), bm);
+        std::memcpy(hs + os, pl.seg_start.data(), bs);
+        std::memcpy(hs + ov, pl.seg_vend.data(), bs);
+        uint32_t max_t = 0;
+        for (const Item &it : pl.items)
+            max_t = std::max(max_t, (it.v_end - it.v_begin + BC - 1) / BC);
+        std::vector<uint64_t> start(max_t + 2, 0);
+        for (const Item &it : pl.items)
+            ++start[max_t - (it.v_end - it.v_begin + BC - 1) / BC + 1];
+        for (uint32_t t = 0; t <= max_t; ++t)
+            start[t + 1] += start[t];
+        Item *sorted = reinterpret_cast<Item *>(hs + oi);
+        for (const Item &it : pl.items)
+            sorted[start[max_t - (it.v_end - it.v_begin + BC - 1) / BC]++] = it;
+        HIPCHECK(hipMemcpyAsync(ws.jobs.p, hs + oj, bj, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.items.p, hs + oi, bi, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.mitems.p, hs + om, bm, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.seg_start.p, hs + os, bs, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(ws.seg_vend.p, hs + ov, bs, hipMemcpyHostToDevice, ws.stream));
     }
-    HIPCHECK(hipStreamSynchronize(ws.stream));
+    HIPCHECK(hipStreamSynchronize(ws.stream)); // the pinned staging is reused by the next call
     if (st)
         st->h2d_ms += ms_since(t_h2d);
     if (pl.jobs.empty())

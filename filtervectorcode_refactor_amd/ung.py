@@ -153,7 +153,8 @@ class HipContext:
         G = group_begin.shape[0] - 2
         edge_ptr = np.zeros(G + 2, np.uint32)
         n = C.c_uint64(0)
-        cap = max(1024, int(group_begin[-1]) // 8)
+        # the capacity the last call needed (a retry repeats the host planning)
+        cap = max(1024, int(group_begin[-1]) // 2, getattr(self, "_addl_cap", 0))
         while True:
             ef = np.empty(cap, np.uint32)
             et = np.empty(cap, np.uint32)
@@ -162,6 +163,7 @@ class HipContext:
                                                    ptr(edge_ptr), ptr(ef), ptr(et), cap, C.byref(n), C.byref(st))
             if rc == _lib.UNG_HIP_EINVAL and n.value > cap:
                 cap = int(n.value)
+                self._addl_cap = cap
                 continue
             check(rc)
             return edge_ptr, ef[: n.value].copy(), et[: n.value].copy(), st.as_dict()
