@@ -1401,6 +1401,123 @@ __global__ void ung_addl_mark_kernel(const uint32_t *__restrict__ ids, uint32_t 
     }
 }
 
+// Additional edges, step 2: per LNG entry p = (C, X) left unreached, the query rows
+// m = min(|C|, ceil(num_cross / per)) and edges m * per it adds, per = min(|X|, num_cross/2)
+// (src/uni_nav_graph_cross_edges.cpp:543-562: vectors of C in order, per edges each, until
+// num_cross are appended); 0 for reached entries and for entries of no group (eg = 0).
+// cnt[0] += scored (query, candidate) pairs, cnt[1] += entries that add edges.
+__global__ void ung_addl_count_kernel(const uint32_t *__restrict__ gb, const uint32_t *__restrict__ oi,
+                                      const uint32_t *__restrict__ eg, const uint32_t *__restrict__ reached,
+                                      uint32_t E, uint32_t num_cross, uint32_t *__restrict__ rows,
+                                      uint32_t *__restrict__ edges, unsigned long long *__restrict__ cnt)
+{
+    unsigned long long my_pairs = 0, my_entries = 0;
+    for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < E; p += gridDim.x * blockDim.x) {
+        uint32_t m = 0, per = 0;
+        const uint32_t c = eg[p];
+        if (!reached[p] && c != 0) {
+            const uint32_t x = oi[p];
+            const uint32_t nc = gb[c + 1] - gb[c], nx = gb[x + 1] - gb[x];
+            per = min(nx, num_cross / 2u);
+            if (per > 0 && nc > 0)
+                m = min(nc, (num_cross + per - 1) / per);
+            my_pairs += (unsigned long long)m * nx;
+            my_entries += m > 0;
+        }
+        rows[p] = m;
+        edges[p] = m * per;
+    }
+    if (my_pairs)
+        atomicAdd(&cnt[0], my_pairs);
+    if (my_entries)
+        atomicAdd(&cnt[1], my_entries);
+}
+
+// Additional edges, step 3: one wave per query row r (entry p = the last with row_off[p] <=
+// r, vector j = r - row_off[p] of C): an exact scan of X's range in the reference's
+// summation order and (dist, id) order, the first `per` results written to their final
+// place in the per-group edge lists (entries in LNG order, vectors, ranks).
+struct AddlParams {
+    const float *X;
+    uint32_t d;
+    const uint32_t *gb, *oi, *eg;
+    const uint32_t *row_off, *edge_off; // [E+1] exclusive scans
+    uint32_t E;
+    uint32_t per_max;
+    uint32_t *from, *to;
+};
+
+__global__ __launch_bounds__(64) void ung_addl_scan_kernel(AddlParams A)
+{
+    __shared__ float sd[64][33];
+    __shared__ uint32_t si[64][33];
+    const int lane = threadIdx.x;
+    const uint32_t R = A.row_off[A.E];
+    for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
+        uint32_t lo = 0, hi = A.E - 1; // the last entry p with row_off[p] <= r
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) >> 1;
+            if (A.row_off[mid] <= r)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        const uint32_t p = lo, j = r - A.row_off[p];
+        const uint32_t c = A.eg[p], x = A.oi[p];
+        const uint32_t q = A.gb[c] + j;
+        const uint32_t x0 = A.gb[x], x1 = A.gb[x + 1];
+        const uint32_t per = min(x1 - x0, A.per_max);
+        const float *qv = A.X + (size_t)q * A.d;
+        int32_t size = 0;
+        for (uint32_t g = x0 + (uint32_t)lane; g < x1; g += 64) {
+            const float dist = l2_ref_lane(qv, A.X + (size_t)g * A.d, A.d);
+            if (size == (int32_t)per && !cand_less(dist, g, sd[lane][size - 1], si[lane][size - 1]))
+                continue;
+            int32_t pos = size < (int32_t)per ? size : (int32_t)per - 1;
+            while (pos > 0 && cand_less(dist, g, sd[lane][pos - 1], si[lane][pos - 1])) {
+                sd[lane][pos] = sd[lane][pos - 1];
+                si[lane][pos] = si[lane][pos - 1];
+                --pos;
+            }
+            sd[lane][pos] = dist;
+            si[lane][pos] = g;
+            if (size < (int32_t)per)
+                ++size;
+        }
+        int head = 0;
+        const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
+        for (uint32_t t = 0; t < per; ++t) {
+            const float hd = head < size ? sd[lane][head] : INFINITY;
+            const uint32_t hi2 = head < size ? si[lane][head] : NONE;
+            float bd = hd;
+            uint32_t bi = hi2;
+            for (int off = 32; off > 0; off >>= 1) {
+                const float od = __shfl_xor(bd, off);
+                const uint32_t oi2 = __shfl_xor(bi, off);
+                if (cand_less(od, oi2, bd, bi)) {
+                    bd = od;
+                    bi = oi2;
+                }
+            }
+            if (bi != NONE && hi2 == bi)
+                ++head;
+            if (lane == 0) {
+                A.from[o + t] = q;
+                A.to[o + t] = bi;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// edge_ptr[c] = first edge of group c: the edge offset of its first LNG entry.
+__global__ void ung_addl_ptr_kernel(const uint32_t *__restrict__ op, const uint32_t *__restrict__ edge_off,
+                                    uint32_t G, uint32_t *__restrict__ edge_ptr)
+{
+    for (uint32_t c = blockIdx.x * blockDim.x + threadIdx.x; c <= G + 1; c += gridDim.x * blockDim.x)
+        edge_ptr[c] = c == 0 ? 0u : edge_off[op[c]];
+}
+
 // Exact-anchor row packing (src/tagore_graph_builder.cu:727-794), one thread per row.
 struct PackParams {
     const Job *jobs;
@@ -1848,9 +1965,12 @@ struct ung_hip_ctx {
     DevBuf<uint32_t> rv_cnt, rv_fill, rv_src;
     DevBuf<float> rv_dist;
     DevBuf<unsigned char> rv_tmp;
-    // additional edges: group ranges, LNG rows, point groups, reached flags, result rows
-    DevBuf<uint32_t> a_gb, a_op, a_oi, a_pg, a_reached, a_ids;
-    DevBuf<int32_t> a_size;
+    // additional edges: group ranges, LNG rows, point groups, reached flags, entry groups,
+    // per-entry row/edge counts (scanned in place), group offsets, edge lists, counters
+    DevBuf<uint32_t> a_gb, a_op, a_oi, a_pg, a_reached, a_eg, a_rows, a_edges, a_ptr, a_from, a_to;
+    DevBuf<unsigned long long> a_cnt;
+    DevBuf<unsigned char> a_tmp;
+    HostBuf a_stage;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
     bool force_wide = false;
     // test hook: UNG_HIP_EPS_SCALE=s (s >= 1) at create widens the certification error
@@ -2520,10 +2640,12 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
 }
 
 // Additional edges (src/uni_nav_graph_cross_edges.cpp:442-596, exact branch :543-562)
-// from the resident cross-edge rows: reached out-groups are marked on the device, the
-// missing (C, X) pairs become one job each (C's first m vectors against X's range, m
-// vectors of min(|X|, num_cross/2) edges each until num_cross are reached), scored
-// exactly by the fallback kernel, and compacted into per-group edge lists on the host.
+// from the resident cross-edge rows, planned and scored on the device: reached out-groups
+// are marked, every missing (C, X) entry counts its query rows (C's first m vectors, m
+// vectors of min(|X|, num_cross/2) edges each until num_cross are reached) and edges, two
+// exclusive scans give each row its place in the per-group edge lists, and one wave per
+// row writes its exact nearest members of X there.  The host reads back three totals and
+// the finished lists.
 int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
                       const uint32_t *out_idx, uint32_t num_cross, uint32_t *edge_ptr, uint32_t *edge_from,
                       uint32_t *edge_to, uint64_t capacity, uint64_t *n_edges, ung_hip_stats *st)
@@ -2544,9 +2666,9 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         set_error("ung_hip_additional_edges: null argument");
         return UNG_HIP_EINVAL;
     }
-    if ((uint64_t)group_begin[G + 1] != ctx->N) {
-        set_error("ung_hip_additional_edges: group_begin[G+1]=%u but %llu vectors are prepared", group_begin[G + 1],
-                  (unsigned long long)ctx->N);
+    if ((uint64_t)group_begin[G + 1] != ctx->N || group_begin[1] != 0) {
+        set_error("ung_hip_additional_edges: group_begin[1]=%u, group_begin[G+1]=%u but %llu vectors are prepared",
+                  group_begin[1], group_begin[G + 1], (unsigned long long)ctx->N);
         return UNG_HIP_EINVAL;
     }
     for (uint32_t g = 1; g <= G; ++g)
@@ -2560,154 +2682,120 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
             set_error("ung_hip_additional_edges: out_idx entry %u out of range 1..%u", out_idx[p], G);
             return UNG_HIP_EINVAL;
         }
+    // an entry adds at most num_cross query rows and fewer than 3 * num_cross / 2 edges:
+    // both running totals stay 32-bit
+    if ((uint64_t)E * 2u * num_cross >= 0xFFFFFFFFull) {
+        set_error("ung_hip_additional_edges: %u LNG entries x num_cross=%u exceed 32-bit edge offsets", E, num_cross);
+        return UNG_HIP_EINVAL;
+    }
     if ((rc = set_device(ctx)))
         return rc;
     const auto t0 = clk::now();
     const uint64_t N = ctx->N;
-    const uint32_t per_max = num_cross / 2;
-    std::vector<uint32_t> reached(E, 0u);
-    if (E > 0 && per_max > 0) {
-        if ((rc = ctx->a_gb.ensure(G + 2)) || (rc = ctx->a_op.ensure(G + 2)) || (rc = ctx->a_oi.ensure(E)) ||
-            (rc = ctx->a_pg.ensure(N)) || (rc = ctx->a_reached.ensure(E)))
-            return rc;
-        HIPCHECK(hipMemcpyAsync(ctx->a_gb.p, group_begin, (G + 2) * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->a_op.p, out_ptr, (G + 2) * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->a_oi.p, out_idx, E * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        hipLaunchKernelGGL(ung_zero_u32_kernel, dim3((E + 255) / 256), dim3(256), 0, ctx->stream, ctx->a_reached.p, E);
-        HIPCHECK(hipGetLastError());
-        hipLaunchKernelGGL(ung_point_group_kernel, dim3(std::max<uint32_t>(1u, std::min<uint32_t>(G, 65535u))), dim3(256),
-                           0, ctx->stream, ctx->a_gb.p, G, ctx->a_pg.p);
-        HIPCHECK(hipGetLastError());
-        hipLaunchKernelGGL(ung_addl_mark_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, ctx->stream,
+    hipStream_t sm0 = ctx->stream;
+    // inputs through pinned staging
+    if ((rc = ctx->a_gb.ensure(G + 2)) || (rc = ctx->a_op.ensure(G + 2)) || (rc = ctx->a_oi.ensure(E + 1)) ||
+        (rc = ctx->a_pg.ensure(N)) || (rc = ctx->a_reached.ensure(E + 1)) || (rc = ctx->a_eg.ensure(E + 1)) ||
+        (rc = ctx->a_rows.ensure(E + 1)) || (rc = ctx->a_edges.ensure(E + 1)) || (rc = ctx->a_ptr.ensure(G + 2)) ||
+        (rc = ctx->a_cnt.ensure(2)) || (rc = ctx->a_stage.ensure(((size_t)2 * (G + 2) + E + 4) * sizeof(uint32_t))))
+        return rc;
+    uint32_t *hs = static_cast<uint32_t *>(ctx->a_stage.p);
+    std::memcpy(hs, group_begin, (G + 2) * sizeof(uint32_t));
+    std::memcpy(hs + (G + 2), out_ptr, (G + 2) * sizeof(uint32_t));
+    if (E)
+        std::memcpy(hs + 2 * (G + 2), out_idx, E * sizeof(uint32_t));
+    HIPCHECK(hipMemcpyAsync(ctx->a_gb.p, hs, (G + 2) * sizeof(uint32_t), hipMemcpyHostToDevice, sm0));
+    HIPCHECK(hipMemcpyAsync(ctx->a_op.p, hs + (G + 2), (G + 2) * sizeof(uint32_t), hipMemcpyHostToDevice, sm0));
+    if (E)
+        HIPCHECK(hipMemcpyAsync(ctx->a_oi.p, hs + 2 * (G + 2), E * sizeof(uint32_t), hipMemcpyHostToDevice, sm0));
+    HIPCHECK(hipEventRecord(ctx->ev[0], sm0));
+    // step 1: reached entries; step 2: rows and edges per entry, their scans
+    const unsigned eb = (unsigned)std::min<uint64_t>((E + 256) / 256, 65535);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(eb), dim3(256), 0, sm0, ctx->a_reached.p, E + 1);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(eb), dim3(256), 0, sm0, ctx->a_eg.p, E + 1);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, sm0, reinterpret_cast<uint32_t *>(ctx->a_cnt.p), 4u);
+    hipLaunchKernelGGL(ung_point_group_kernel, dim3(std::max<uint32_t>(1u, std::min<uint32_t>(G, 65535u))), dim3(256),
+                       0, sm0, ctx->a_gb.p, G, ctx->a_pg.p);
+    hipLaunchKernelGGL(ung_point_group_kernel, dim3(std::max<uint32_t>(1u, std::min<uint32_t>(G, 65535u))), dim3(256),
+                       0, sm0, ctx->a_op.p, G, ctx->a_eg.p);
+    HIPCHECK(hipGetLastError());
+    if (E > 0 && num_cross / 2 > 0) {
+        hipLaunchKernelGGL(ung_addl_mark_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, sm0,
                            ctx->cross.ids.p, ctx->cross.k, num_cross, ctx->a_pg.p, N, ctx->a_op.p, ctx->a_oi.p,
                            ctx->a_reached.p);
         HIPCHECK(hipGetLastError());
-        HIPCHECK(hipMemcpyAsync(reached.data(), ctx->a_reached.p, E * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
-        HIPCHECK(hipStreamSynchronize(ctx->stream));
     }
-    // one job per missing (C, X): C's first m vectors against X's range
-    std::vector<Job> jobs;
-    std::vector<uint32_t> seg_start, seg_vend, job_c, job_per;
-    std::vector<uint2> rows;
-    uint64_t total_edges = 0, pairs = 0;
-    if (per_max > 0) {
-        for (uint32_t c = 1; c <= G; ++c) {
-            const uint32_t nc = group_begin[c + 1] - group_begin[c];
-            for (uint32_t p = out_ptr[c]; p < out_ptr[c + 1]; ++p) {
-                if (reached[p])
-                    continue;
-                const uint32_t x = out_idx[p];
-                const uint32_t nx = group_begin[x + 1] - group_begin[x];
-                const uint32_t per = std::min(nx, per_max);
-                if (per == 0 || nc == 0)
-                    continue;
-                const uint32_t m = std::min<uint32_t>(nc, (num_cross + per - 1) / per);
-                Job jb{};
-                jb.q_begin = group_begin[c];
-                jb.q_count = m;
-                jb.seg_begin = (uint32_t)seg_start.size();
-                jb.seg_count = 1;
-                jb.n_cand = nx;
-                jb.n_split = 1;
-                jb.split_v = nx;
-                jb.out_row = (uint32_t)rows.size();
-                seg_start.push_back(group_begin[x]);
-                seg_vend.push_back(nx);
-                for (uint32_t j = 0; j < m; ++j)
-                    rows.push_back(make_uint2((uint32_t)jobs.size(), j));
-                jobs.push_back(jb);
-                job_c.push_back(c);
-                job_per.push_back(per);
-                total_edges += (uint64_t)m * per;
-                pairs += (uint64_t)m * nx;
-                if (rows.size() >= 0xFFFFFFFFull) {
-                    set_error("ung_hip_additional_edges: more than 2^32 query rows");
-                    return UNG_HIP_EINVAL;
-                }
-            }
-        }
-    }
+    hipLaunchKernelGGL(ung_addl_count_kernel, dim3(eb), dim3(256), 0, sm0, ctx->a_gb.p, ctx->a_oi.p, ctx->a_eg.p,
+                       ctx->a_reached.p, E, num_cross, ctx->a_rows.p, ctx->a_edges.p, ctx->a_cnt.p);
+    HIPCHECK(hipGetLastError());
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, sm0, ctx->a_rows.p + E, 1u);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, sm0, ctx->a_edges.p + E, 1u);
+    size_t tmp = 0, tmp2 = 0;
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp, ctx->a_rows.p, ctx->a_rows.p, (int)(E + 1), sm0));
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp2, ctx->a_edges.p, ctx->a_edges.p, (int)(E + 1), sm0));
+    if ((rc = ctx->a_tmp.ensure(std::max(tmp, tmp2) + 1)))
+        return rc;
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(ctx->a_tmp.p, tmp, ctx->a_rows.p, ctx->a_rows.p, (int)(E + 1), sm0));
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(ctx->a_tmp.p, tmp2, ctx->a_edges.p, ctx->a_edges.p, (int)(E + 1), sm0));
+    uint32_t totals[2] = {0, 0};
+    unsigned long long cnt[2] = {0, 0};
+    HIPCHECK(hipMemcpyAsync(&totals[0], ctx->a_rows.p + E, sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
+    HIPCHECK(hipMemcpyAsync(&totals[1], ctx->a_edges.p + E, sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
+    HIPCHECK(hipMemcpyAsync(cnt, ctx->a_cnt.p, sizeof(cnt), hipMemcpyDeviceToHost, sm0));
+    HIPCHECK(hipStreamSynchronize(sm0));
+    const uint32_t R = totals[0];
+    const uint64_t total_edges = totals[1];
     *n_edges = total_edges;
+    if (st)
+        st->plan_ms += ms_since(t0);
     if (total_edges > capacity || (total_edges > 0 && (!edge_from || !edge_to))) {
         set_error("ung_hip_additional_edges: %llu edges need capacity (got %llu)", (unsigned long long)total_edges,
                   (unsigned long long)capacity);
         return UNG_HIP_EINVAL;
     }
-    if (st) {
-        st->plan_ms += ms_since(t0);
-        st->rows += rows.size();
-        st->pairs += pairs;
-        st->work_items += jobs.size();
-    }
-    std::vector<uint32_t> ids;
-    std::vector<int32_t> size;
-    if (!rows.empty()) {
-        const uint64_t R = rows.size();
-        if ((rc = ctx->ws[0].jobs.ensure(jobs.size())) || (rc = ctx->ws[0].seg_start.ensure(seg_start.size())) ||
-            (rc = ctx->ws[0].seg_vend.ensure(seg_vend.size())) || (rc = ctx->ws[0].flagged.ensure(R)) ||
-            (rc = ctx->ws[0].flag_count.ensure(2)) || (rc = ctx->a_ids.ensure(R * per_max)) || (rc = ctx->a_size.ensure(R)))
-            return rc;
-        const uint32_t nrows = (uint32_t)R;
-        HIPCHECK(hipMemcpyAsync(ctx->ws[0].jobs.p, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->ws[0].seg_start.p, seg_start.data(), seg_start.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->ws[0].seg_vend.p, seg_vend.data(), seg_vend.size() * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->ws[0].flagged.p, rows.data(), R * sizeof(uint2), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(ctx->ws[0].flag_count.p, &nrows, sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream));
-        HIPCHECK(hipEventRecord(ctx->ev[0], ctx->stream));
-        FallbackParams F{};
-        F.X = ctx->X;
-        F.d = ctx->d;
-        F.k = per_max;
-        F.jobs = ctx->ws[0].jobs.p;
-        F.seg_start = ctx->ws[0].seg_start.p;
-        F.seg_vend = ctx->ws[0].seg_vend.p;
-        F.flag_count = ctx->ws[0].flag_count.p;
-        F.flagged = ctx->ws[0].flagged.p;
-        F.splits = 1;
-        F.out_ids = ctx->a_ids.p;
-        F.out_dist = nullptr;
-        F.out_size = ctx->a_size.p;
-        hipLaunchKernelGGL(ung_fallback_kernel, dim3(std::min<uint32_t>(nrows, 8192u)), dim3(64), 0, ctx->stream, F);
+    // step 3: the scans, written in place; per-group offsets
+    if ((rc = ctx->a_from.ensure(total_edges + 1)) || (rc = ctx->a_to.ensure(total_edges + 1)))
+        return rc;
+    HIPCHECK(hipEventRecord(ctx->ev[1], sm0));
+    if (R > 0) {
+        AddlParams A{};
+        A.X = ctx->X;
+        A.d = ctx->d;
+        A.gb = ctx->a_gb.p;
+        A.oi = ctx->a_oi.p;
+        A.eg = ctx->a_eg.p;
+        A.row_off = ctx->a_rows.p;
+        A.edge_off = ctx->a_edges.p;
+        A.E = E;
+        A.per_max = num_cross / 2;
+        A.from = ctx->a_from.p;
+        A.to = ctx->a_to.p;
+        hipLaunchKernelGGL(ung_addl_scan_kernel, dim3(std::min<uint32_t>(R, 65536u)), dim3(64), 0, sm0, A);
         HIPCHECK(hipGetLastError());
-        HIPCHECK(hipEventRecord(ctx->ev[1], ctx->stream));
-        ids.resize(R * per_max);
-        size.resize(R);
-        HIPCHECK(hipMemcpyAsync(ids.data(), ctx->a_ids.p, ids.size() * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
-        HIPCHECK(hipMemcpyAsync(size.data(), ctx->a_size.p, R * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
-        HIPCHECK(hipStreamSynchronize(ctx->stream));
-        if (st) {
-            float ms = 0;
-            HIPCHECK(hipEventElapsedTime(&ms, ctx->ev[0], ctx->ev[1]));
-            st->fallback_ms += ms;
-            st->kernel_ms += ms;
-        }
     }
-    // compact into per-group lists in the reference's append order
-    uint64_t n = 0;
-    size_t ji = 0;
-    edge_ptr[0] = edge_ptr[1] = 0;
-    for (uint32_t c = 1; c <= G; ++c) {
-        for (; ji < jobs.size() && job_c[ji] == c; ++ji) {
-            const Job &jb = jobs[ji];
-            for (uint32_t j = 0; j < jb.q_count; ++j) {
-                const uint32_t r = jb.out_row + j;
-                const uint32_t cnt = std::min<uint32_t>((uint32_t)size[r], job_per[ji]);
-                for (uint32_t t = 0; t < cnt; ++t) {
-                    edge_from[n] = jb.q_begin + j;
-                    edge_to[n] = ids[(size_t)r * per_max + t];
-                    ++n;
-                }
-            }
-        }
-        edge_ptr[c + 1] = (uint32_t)n;
+    hipLaunchKernelGGL(ung_addl_ptr_kernel, dim3((G + 2 + 255) / 256), dim3(256), 0, sm0, ctx->a_op.p, ctx->a_edges.p,
+                       G, ctx->a_ptr.p);
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipEventRecord(ctx->ev[2], sm0));
+    const auto t1 = clk::now();
+    HIPCHECK(hipMemcpyAsync(edge_ptr, ctx->a_ptr.p, (G + 2) * sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
+    if (total_edges) {
+        HIPCHECK(hipMemcpyAsync(edge_from, ctx->a_from.p, total_edges * sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
+        HIPCHECK(hipMemcpyAsync(edge_to, ctx->a_to.p, total_edges * sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
     }
-    if (n != total_edges) {
-        set_error("ung_hip_additional_edges: %llu edges produced, %llu expected", (unsigned long long)n,
-                  (unsigned long long)total_edges);
-        return UNG_HIP_EDEVICE;
-    }
-    if (st)
+    HIPCHECK(hipStreamSynchronize(sm0));
+    if (st) {
+        float k1 = 0, k2 = 0;
+        HIPCHECK(hipEventElapsedTime(&k1, ctx->ev[0], ctx->ev[1]));
+        HIPCHECK(hipEventElapsedTime(&k2, ctx->ev[1], ctx->ev[2]));
+        st->fallback_ms += k2;
+        st->kernel_ms += k1 + k2;
+        st->d2h_ms += ms_since(t1);
+        st->rows += R;
+        st->pairs += cnt[0];
+        st->work_items += cnt[1];
         st->wall_ms += ms_since(t0);
+    }
     return UNG_HIP_OK;
 }
 
@@ -2905,8 +2993,15 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     ctx->a_oi.release();
     ctx->a_pg.release();
     ctx->a_reached.release();
-    ctx->a_ids.release();
-    ctx->a_size.release();
+    ctx->a_eg.release();
+    ctx->a_rows.release();
+    ctx->a_edges.release();
+    ctx->a_ptr.release();
+    ctx->a_from.release();
+    ctx->a_to.release();
+    ctx->a_cnt.release();
+    ctx->a_tmp.release();
+    ctx->a_stage.release();
     for (auto &ev : ctx->ev)
         if (ev)
             (void)hipEventDestroy(ev);
