@@ -130,7 +130,8 @@ int ung_hip_download_cross(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist,
  * lists of the reference, edges of C in [edge_ptr[C], edge_ptr[C+1])), edge_from /
  * edge_to global new ids, in the reference's append order.  capacity = entries of
  * edge_from/edge_to; *n_edges receives the count; UNG_HIP_EINVAL (nothing written) when
- * capacity is too small. */
+ * capacity is too small.  group_begin[1] must be 0 and out_ptr[G+1] * 2 * num_cross must
+ * stay below 2^32 (32-bit edge offsets); UNG_HIP_EINVAL otherwise. */
 int ung_hip_additional_edges(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
                              const uint32_t *out_ptr, const uint32_t *out_idx, uint32_t num_cross,
                              uint32_t *edge_ptr, uint32_t *edge_from, uint32_t *edge_to,
