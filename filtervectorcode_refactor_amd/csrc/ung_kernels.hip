@@ -290,6 +290,14 @@ __device__ __forceinline__ void wave_argmin(float &d, uint32_t &i)
 // ---------------------------------------------------------------------------
 // select kernel
 // ---------------------------------------------------------------------------
+// End-of-item reduction area: the queues of 64 queries.
+struct SelectRed {
+    float ed[64][129];   // entry distances (approx, then exact); stride padded
+    uint32_t ei[64][129];
+    float alist[64][4];  // per queue: bound on every candidate it did not keep
+    float drop[64];      // smallest queued value not written to the partial row
+};
+
 struct alignas(16) SelectSmem {
     union {
         struct {
@@ -297,12 +305,7 @@ struct alignas(16) SelectSmem {
             float4 qs[2][BQ][LDSW / 4];
             float4 xs[2][BC][LDSW / 4];
         } p;
-        struct {
-            float ed[64][129];   // entry distances (approx, then exact); stride padded
-            uint32_t ei[64][129];
-            float alist[64][4];  // per queue: bound on every candidate it did not keep
-            float drop[64];      // smallest queued value not written to the partial row
-        } r;
+        SelectRed r;
     } u;
     uint32_t rowid[3][BC]; // candidate ids of tiles t%3 (ring: built one tile ahead; NONE = padding)
     float4 nhx[3][BC / 4]; // their -|x|^2/2 (-inf for padding rows), 4 rows per float4
@@ -310,6 +313,28 @@ struct alignas(16) SelectSmem {
     float tau[2][2][BQ];   // [tile parity][candidate wave][query]: a wave's queue threshold
 };
 static_assert(BQ == BC, "the epilogue staging addresses assume square panels");
+
+// Register-query layout (dp = 128, two query columns per lane): a lane keeps the high
+// bf16 words of its query columns for all 8 k-blocks in registers for the whole item,
+// and the low words of the item's queries stay resident in LDS; per step only the
+// candidate chunk is loaded and staged.  LDS traffic per step and wave: 8 KB of
+// candidate operands + 4 KB of query low words + 4 KB of staging writes, against 16 +
+// 8 KB when both panels are restaged every step.
+constexpr int QR_NK = 4;              // chunks of 32 dimensions (dp = 128)
+constexpr int QLO_W = QR_NK * 16 + 4; // words per resident low-word query row (padded)
+struct alignas(16) SelectSmemQ {
+    union {
+        struct {
+            float4 xs[2][BC][LDSW / 4];
+            float4 qlo[BQ][QLO_W / 4];
+        } p;
+        SelectRed r;
+    } u;
+    uint32_t rowid[3][BC];
+    float4 nhx[3][BC / 4];
+    float qn[BQ];
+    float tau[2][2][BQ];
+};
 // flat float offsets inside SelectSmem::u.p
 constexpr int PANEL_X = 2 * BQ * LDSW; // start of xs relative to qs
 constexpr int ROW32 = 32 * LDSW;       // 32 panel rows
@@ -380,7 +405,8 @@ __device__ __forceinline__ uint32_t cursor_id(RowCursor &c, const SelectParams &
 // Row ids of the candidate tile starting at virtual index v0 into ring slot `slot`;
 // returns the row's |x|^2 (+inf for padding rows), a load the caller consumes later
 // (finish_rowids), so its latency overlaps other work.
-__device__ __forceinline__ float start_rowids(SelectSmem &sm, int slot, RowCursor &cur, const SelectParams &P,
+template <class Smem>
+__device__ __forceinline__ float start_rowids(Smem &sm, int slot, RowCursor &cur, const SelectParams &P,
                                               const Job &jb, uint32_t v0, uint32_t v_end, int tid)
 {
     float nx = INFINITY;
@@ -396,7 +422,8 @@ __device__ __forceinline__ float start_rowids(SelectSmem &sm, int slot, RowCurso
     return nx;
 }
 
-__device__ __forceinline__ void finish_rowids(SelectSmem &sm, int slot, float nx, int tid)
+template <class Smem>
+__device__ __forceinline__ void finish_rowids(Smem &sm, int slot, float nx, int tid)
 {
     if (tid < BC)
         reinterpret_cast<float *>(sm.nhx[slot])[tid] = -0.5f * nx; // -|x|^2/2 (exact scaling)
@@ -539,16 +566,17 @@ constexpr int select_threads()
     return NB == 2 ? NTHREADS : 2 * NTHREADS;
 }
 
-template <int LT, int MODE, bool EXCL, int NB>
+template <int LT, int MODE, bool EXCL, int NB, bool QR>
 __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
 {
     static_assert(NB == 1 || NB == 2, "one or two query columns per lane");
+    static_assert(!QR || (NB == 2 && LT == 8 && MODE == LOAD_BUF32), "register-query layout: NB = 2, LT = 8, 32-bit loads");
     constexpr int NTH = select_threads<NB>();
     constexpr int WN = 4 / NB;         // query waves
     constexpr int QW = 32 * NB;        // query columns per wave
     constexpr int RSTEP = NTH / 8;     // loader row step
     constexpr int LM = BQ / RSTEP;     // rows per thread and panel
-    __shared__ SelectSmem sm;
+    __shared__ typename std::conditional<QR, SelectSmemQ, SelectSmem>::type sm;
     __shared__ typename std::conditional<NB == 1, SelectStage, NoStage>::type stage;
     __shared__ uint32_t item_slot;
     const uint32_t logical = take_item(P.item_ctr, &item_slot);
@@ -564,7 +592,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     // buffer descriptor of the wide mode in scalar registers
     const uint32_t q0 = __builtin_amdgcn_readfirstlane(jb.q_begin + it.q_off);
     const uint32_t qcnt = __builtin_amdgcn_readfirstlane(it.q_cnt);
-    const uint32_t dp = P.dp;
+    const uint32_t dp = QR ? (uint32_t)(QR_NK * KC) : P.dp;
     const uint32_t *__restrict__ XS = P.xs;
 
     if (tid < BQ)
@@ -608,6 +636,29 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     const uint32_t qoff = MODE == LOAD_BUF32 ? ((q0 + (uint32_t)lr0) * dp + (uint32_t)c4) * 4u
                                              : ((uint32_t)lr0 * dp + (uint32_t)c4) * 4u;
 
+    // register-query layout: the high words of this lane's query columns (k-block kb:
+    // chunk kb/2, float4 column 2*(kb%2) + h of the chunk row) and the low words of all
+    // the item's queries (float4 column 4*chunk + c of row q) into LDS
+    [[maybe_unused]] bf16x8 bhr[2 * QR_NK][NB];
+    if constexpr (QR) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const uint32_t row = q0 + (uint32_t)(wn * QW + 32 * nb + r);
+#pragma unroll
+            for (int kb = 0; kb < 2 * QR_NK; ++kb)
+                bhr[kb][nb] = __builtin_bit_cast(
+                    bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                xres, (row * dp + (uint32_t)((kb >> 1) * KC + (2 * (kb & 1) + h) * 4)) * 4u, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < BQ * QR_NK * 4 / NTH; ++i) {
+            const int idx = tid + NTH * i;
+            const int q = idx >> 4, f = idx & 15; // f = 4*chunk + float4 column of the low words
+            const uint32_t off = ((q0 + (uint32_t)q) * dp + (uint32_t)((f >> 2) * KC + 16 + (f & 3) * 4)) * 4u;
+            sm.u.p.qlo[q][f] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
+        }
+    }
+
     __syncthreads();
     float qnv[NB];
 #pragma unroll
@@ -633,12 +684,14 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 xrow[m] = XS + (size_t)g * dp + c4;
         }
     };
-    float4 rq[LM], rx[LM]; // raw split words (bf16 pairs), typed for 16-byte moves
+    [[maybe_unused]] float4 rq[LM];
+    float4 rx[LM]; // raw split words (bf16 pairs), typed for 16-byte moves
     auto load_chunk = [&](uint32_t kc) {
 #pragma unroll
         for (int m = 0; m < LM; ++m) {
             if constexpr (MODE == LOAD_BUF32) {
-                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff, kc * 4u + m * qrow_step, 0));
+                if constexpr (!QR)
+                    rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
             } else {
                 rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff, kc * 4u + m * qrow_step, 0));
@@ -658,15 +711,18 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     set_xrows(0);
     load_chunk(0);
 
-    uint32_t tile = 0, kc = 0;
+    uint32_t tile = 0, kc_state = 0;
     int slot = 0;
     float pend_nx = INFINITY;
-    for (uint32_t s = 0; s < total; ++s) {
+    // one step; kcv: the chunk index, a compile-time constant in the register-query layout
+    auto step = [&](uint32_t s, auto kcv) __attribute__((always_inline)) {
+        const uint32_t kc = (uint32_t)kcv;
         const int buf = (int)(s & 1u);
         const int next_slot = slot == 2 ? 0 : slot + 1;
 #pragma unroll
         for (int m = 0; m < LM; ++m) {
-            sm.u.p.qs[buf][lr0 + RSTEP * m][c4 >> 2] = rq[m];
+            if constexpr (!QR)
+                sm.u.p.qs[buf][lr0 + RSTEP * m][c4 >> 2] = rq[m];
             sm.u.p.xs[buf][lr0 + RSTEP * m][c4 >> 2] = rx[m];
         }
         if (nk == 1 && tile + 1 < ntiles)
@@ -705,8 +761,14 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 }
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    bh[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * QW + 32 * nb + r][ch]);
-                    bl[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * QW + 32 * nb + r][ch + 4]);
+                    if constexpr (QR) {
+                        constexpr int KCI = decltype(kcv)::value;
+                        bh[nb] = bhr[2 * KCI + kb][nb];
+                        bl[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qlo[wn * QW + 32 * nb + r][4 * KCI + ch]);
+                    } else {
+                        bh[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * QW + 32 * nb + r][ch]);
+                        bl[nb] = __builtin_bit_cast(bf16x8, sm.u.p.qs[buf][wn * QW + 32 * nb + r][ch + 4]);
+                    }
                 }
                 const bool z = FIRST && kb == 0;
 #pragma unroll
@@ -801,55 +863,11 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     pend[nb] &= self_j[nb] < 32u ? ~(0x80000000u >> self_j[nb]) : 0xFFFFFFFFu;
                 }
             }
-            // One list's 32 values are staged in LDS, so a round reads its element with one
-            // LDS load instead of a register select tree.  NB = 2: each thread owns the 8
-            // panel slots it fills at the next step (buffer buf^1, read by no wave before
-            // the next barrier), slot g holding values 4g..4g+3; NB = 1: its row of the
-            // staging area.
-            float *const pnl = reinterpret_cast<float *>(&sm.u.p);
-            [[maybe_unused]] const int own0 = ((buf ^ 1) * BQ + lr0) * LDSW + c4;
-            auto staged = [&](uint32_t j) -> float & {
-                if constexpr (NB == 1)
-                    return stage.v[tid][j];
-                else
-                    return pnl[own0 + (int)(j >> 4) * PANEL_X + (int)((j >> 2) & 3u) * ROW32 + (int)(j & 3u)];
-            };
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-                for (int g = 0; g < 8; ++g) {
-                    const int mb = g >> 2, g4 = g & 3;
-                    const float4 v = make_float4(acc[mb][nb][4 * g4], acc[mb][nb][4 * g4 + 1],
-                                                 acc[mb][nb][4 * g4 + 2], acc[mb][nb][4 * g4 + 3]);
-                    *reinterpret_cast<float4 *>(&staged(4u * (uint32_t)g)) = v;
-                }
-                uint32_t m = pend[nb];
-                if (tile == 0) {
-                    // first tile: the queues are empty; a sorting network keeps the LT best
-                    // of the tile's 32 candidates instead of up to 32 insertion rounds
-                    float dv[32];
-                    uint32_t iv[32];
-#pragma unroll
-                    for (int g = 0; g < 8; ++g) {
-                        const uint4 ids = *reinterpret_cast<const uint4 *>(&sm.rowid[slot][tile_row(wm, h, 4u * g)]);
-                        const uint32_t idg[4] = {ids.x, ids.y, ids.z, ids.w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int j = 4 * g + e;
-                            float dd = __builtin_fmaf(-2.0f, acc[j >> 4][nb][j & 15], qnv[nb]);
-                            if constexpr (EXCL)
-                                dd = (uint32_t)j == self_j[nb] ? INFINITY : dd;
-                            dv[j] = dd;
-                            iv[j] = dd < INFINITY ? idg[e] : NONE;
-                        }
-                    }
-                    best_of_32<LT>(dv, iv, ld[nb], li[nb]);
-                    m = 0u;
-                }
-                // rounds: each lane inserts at most one pending element per round; the
-                // body is branch-free (an idle lane inserts +inf, which changes nothing)
-                // and the round count is the wave's largest pending count
-                // (binary search on ballots: wave-uniform, no cross-lane data movement)
+            // rounds: each lane inserts at most one pending element of mask m per round; the
+            // body is branch-free (an idle lane inserts +inf, which changes nothing) and the
+            // round count is the wave's largest pending count (binary search on ballots:
+            // wave-uniform, no cross-lane data movement).  staged(j) is element j's value.
+            auto rounds = [&](int nb, uint32_t m, auto &&staged) __attribute__((always_inline)) {
                 const uint32_t np = (uint32_t)__popc(m);
                 uint32_t nr = 0;
 #pragma unroll
@@ -868,6 +886,112 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     dd = (act && dd < fminf(ld[nb][LT - 1], tsh[nb])) ? dd : INFINITY;
                     list_insert<LT>(ld[nb], li[nb], dd, rid);
                 }
+            };
+            // (dist, id) of element j of list nb for the first tile's sorting network
+            auto entry = [&](int nb, int j, uint32_t idg, float &dd, uint32_t &id) __attribute__((always_inline)) {
+                dd = __builtin_fmaf(-2.0f, acc[j >> 4][nb][j & 15], qnv[nb]);
+                if constexpr (EXCL)
+                    dd = (uint32_t)j == self_j[nb] ? INFINITY : dd;
+                id = dd < INFINITY ? idg : NONE;
+            };
+            if constexpr (!QR) {
+                // One list's 32 values are staged in LDS, so a round reads its element with
+                // one LDS load instead of a register select tree.  NB = 2: each thread owns
+                // the 8 panel slots it fills at the next step (buffer buf^1, read by no wave
+                // before the next barrier), slot g holding values 4g..4g+3; NB = 1: its row
+                // of the staging area.
+                float *const pnl = reinterpret_cast<float *>(&sm.u.p);
+                [[maybe_unused]] const int own0 = ((buf ^ 1) * BQ + lr0) * LDSW + c4;
+                auto staged = [&](uint32_t j) -> float & {
+                    if constexpr (NB == 1)
+                        return stage.v[tid][j];
+                    else
+                        return pnl[own0 + (int)(j >> 4) * PANEL_X + (int)((j >> 2) & 3u) * ROW32 + (int)(j & 3u)];
+                };
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) {
+                        const int mb = g >> 2, g4 = g & 3;
+                        const float4 v = make_float4(acc[mb][nb][4 * g4], acc[mb][nb][4 * g4 + 1],
+                                                     acc[mb][nb][4 * g4 + 2], acc[mb][nb][4 * g4 + 3]);
+                        *reinterpret_cast<float4 *>(&staged(4u * (uint32_t)g)) = v;
+                    }
+                    if (tile == 0) {
+                        // first tile: the queues are empty; a sorting network keeps the LT
+                        // best of the tile's 32 candidates instead of up to 32 insertion rounds
+                        float dv[32];
+                        uint32_t iv[32];
+#pragma unroll
+                        for (int g = 0; g < 8; ++g) {
+                            const uint4 ids = *reinterpret_cast<const uint4 *>(&sm.rowid[slot][tile_row(wm, h, 4u * g)]);
+                            const uint32_t idg[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                entry(nb, 4 * g + e, idg[e], dv[4 * g + e], iv[4 * g + e]);
+                        }
+                        best_of_32<LT>(dv, iv, ld[nb], li[nb]);
+                    } else {
+                        rounds(nb, pend[nb], staged);
+                    }
+                }
+            } else {
+                // register-query layout: a thread owns 16 floats of the candidate panel it
+                // fills at the next step (buffer buf^1), so the two 16-candidate halves of
+                // a list are staged and inserted one after the other
+                float *const xsf = reinterpret_cast<float *>(&sm.u.p.xs[0][0][0]);
+                const int own0 = ((buf ^ 1) * BC + lr0) * LDSW + c4;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    if (tile == 0) {
+                        // first tile: best 8 of each half by a sorting network, then the
+                        // best 8 of both
+                        float dv[16];
+                        uint32_t iv[16];
+#pragma unroll
+                        for (int hv = 0; hv < 2; ++hv) {
+#pragma unroll
+                            for (int g = 0; g < 4; ++g) {
+                                const uint4 ids =
+                                    *reinterpret_cast<const uint4 *>(&sm.rowid[slot][tile_row(wm, h, 16u * hv + 4u * g)]);
+                                const uint32_t idg[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+                                for (int e = 0; e < 4; ++e)
+                                    entry(nb, 16 * hv + 4 * g + e, idg[e], dv[4 * g + e], iv[4 * g + e]);
+                            }
+                            sort8(dv, iv, 0);
+                            sort8(dv, iv, 8);
+                            merge8_keep(dv, iv, 0, 8);
+                            if (hv == 1) {
+#pragma unroll
+                                for (int j = 0; j < 8; ++j) {
+                                    dv[8 + j] = ld[nb][j];
+                                    iv[8 + j] = li[nb][j];
+                                }
+                                merge8_keep(dv, iv, 0, 8);
+                            }
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                ld[nb][j] = dv[j];
+                                li[nb][j] = iv[j];
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int hv = 0; hv < 2; ++hv) {
+#pragma unroll
+                            for (int g4 = 0; g4 < 4; ++g4)
+                                *reinterpret_cast<float4 *>(&xsf[own0 + g4 * ROW32]) =
+                                    make_float4(acc[hv][nb][4 * g4], acc[hv][nb][4 * g4 + 1], acc[hv][nb][4 * g4 + 2],
+                                                acc[hv][nb][4 * g4 + 3]);
+                            auto staged = [&](uint32_t j) -> float & {
+                                const uint32_t i = j - 16u * (uint32_t)hv;
+                                return xsf[own0 + (int)(i >> 2) * ROW32 + (int)(i & 3u)];
+                            };
+                            rounds(nb, pend[nb] & (hv == 0 ? 0xFFFF0000u : 0x0000FFFFu), staged);
+                        }
+                    }
+                }
             }
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
@@ -879,11 +1003,22 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
             }
             ++tile;
-            kc = 0;
+            kc_state = 0;
             slot = next_slot;
         } else {
-            ++kc;
+            ++kc_state;
         }
+    };
+    if constexpr (QR) {
+        for (uint32_t s = 0; s < total; s += QR_NK) {
+            step(s, std::integral_constant<uint32_t, 0>{});
+            step(s + 1, std::integral_constant<uint32_t, 1>{});
+            step(s + 2, std::integral_constant<uint32_t, 2>{});
+            step(s + 3, std::integral_constant<uint32_t, 3>{});
+        }
+    } else {
+        for (uint32_t s = 0; s < total; ++s)
+            step(s, kc_state);
     }
 
     // ---- per query: the Lp best queued candidates by approximate distance, and a
@@ -1973,6 +2108,9 @@ struct ung_hip_ctx {
     HostBuf a_stage;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
     bool force_wide = false;
+    // test hook: UNG_HIP_NO_QREG=1 at create keeps the select kernel's restaged query panel
+    // where the register-query layout would apply
+    bool qreg = true;
     // test hook: UNG_HIP_EPS_SCALE=s (s >= 1) at create widens the certification error
     // bound by s, which sends more rows (all, for a huge s) through the exact rescan
     double eps_scale = 1.0;
@@ -2068,14 +2206,24 @@ int launch_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P,
         // queues longer than 8 take the one-column-per-lane layout (two waves per SIMD)
         constexpr int NB = LT <= 8 ? 2 : 1;
         const dim3 g(n), b(select_threads<NB>());
-        if (mode == LOAD_BUF32 && excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true, NB>), g, b, 0, stream, Q);
+        // two columns per lane, dp = 128 and 32-bit loads: the register-query layout
+        const bool qr = NB == 2 && mode == LOAD_BUF32 && ctx->dp == (uint32_t)(QR_NK * KC) && ctx->qreg;
+        if constexpr (NB == 2) {
+            if (qr && excl)
+                hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true, NB, true>), g, b, 0, stream, Q);
+            else if (qr)
+                hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false, NB, true>), g, b, 0, stream, Q);
+        }
+        if (qr)
+            ; // launched above
+        else if (mode == LOAD_BUF32 && excl)
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true, NB, false>), g, b, 0, stream, Q);
         else if (mode == LOAD_BUF32)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false, NB>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false, NB, false>), g, b, 0, stream, Q);
         else if (excl)
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true, NB>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true, NB, false>), g, b, 0, stream, Q);
         else
-            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false, NB>), g, b, 0, stream, Q);
+            hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false, NB, false>), g, b, 0, stream, Q);
         HIPCHECK(hipGetLastError());
     }
     return UNG_HIP_OK;
@@ -2906,6 +3054,8 @@ int ung_hip_create(int device, ung_hip_ctx **out)
     ctx->device = device;
     if (const char *s = std::getenv("UNG_HIP_FORCE_WIDE"))
         ctx->force_wide = s[0] == '1';
+    if (const char *s = std::getenv("UNG_HIP_NO_QREG"))
+        ctx->qreg = s[0] != '1';
     if (const char *s = std::getenv("UNG_HIP_EPS_SCALE")) {
         const double v = std::atof(s);
         ctx->eps_scale = v >= 1.0 ? v : 1.0; // a smaller bound would not be an error bound

@@ -142,7 +142,7 @@ def test_cross_multi_split(ctx, oracle):
 
 
 @pytest.mark.parametrize("n,list_k,dim", [(2, 32, 128), (3, 1, 16), (129, 32, 128), (200, 64, 40), (700, 32, 384),
-                                          (20000, 8, 64)])
+                                          (20000, 8, 64), (300, 6, 128), (1000, 8, 128)])
 def test_intra_edge_cases(ctx, oracle, n, list_k, dim):
     rng = np.random.default_rng(n)
     _say(f"intra edge case n={n} k={list_k} dim={dim}")
