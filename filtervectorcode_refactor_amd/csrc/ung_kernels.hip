@@ -287,6 +287,13 @@ __device__ __forceinline__ void wave_argmin(float &d, uint32_t &i)
     }
 }
 
+// bf16 bits of x rounded to nearest, ties to even (finite x; -inf gives the bf16 -inf).
+__device__ __forceinline__ uint32_t bf16_rne(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
 // ---------------------------------------------------------------------------
 // select kernel
 // ---------------------------------------------------------------------------
@@ -808,18 +815,32 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
             // other wave's of the previous tile).  Any candidate with a >= that value can
             // not be among the query's LT best (one queue already holds LT better ones),
             // and thresholds only decrease, so a stale value is safe.
+            //
+            // The row's -|x|^2/2 is added by one more MFMA per accumulator: the A row
+            // carries it split exactly into three bf16 terms (k = 0..2, lane half 0; a
+            // padding row's -inf in the first term alone), B is 1 there and 0 elsewhere.
+            // The three products sum exactly to the fp32 value, so the MFMA performs the
+            // one rounded fp32 addition acc + (-|x|^2/2).
+            {
+                const float *const nhf = reinterpret_cast<const float *>(&sm.nhx[slot][0]);
+                const bf16x8 bone = __builtin_bit_cast(
+                    bf16x8, make_uint4(h == 0 ? 0x3F803F80u : 0u, h == 0 ? 0x00003F80u : 0u, 0u, 0u));
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+                for (int mb = 0; mb < 2; ++mb) {
+                    const float v = nhf[wm * 64 + 32 * mb + r];
+                    const uint32_t hi = bf16_rne(v);
+                    const float r1 = v - __uint_as_float(hi << 16);
+                    const uint32_t mid = bf16_rne(r1);
+                    const uint32_t lo = bf16_rne(r1 - __uint_as_float(mid << 16));
+                    const bool tail = h == 0 && v > -INFINITY;
+                    const uint32_t w0 = h == 0 ? (hi | (tail ? mid << 16 : 0u)) : 0u;
+                    const uint32_t w1 = tail ? lo : 0u;
+                    const bf16x8 abias = __builtin_bit_cast(bf16x8, make_uint4(w0, w1, 0u, 0u));
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const float4 v = sm.nhx[slot][(wm * 64 + mb * 32 + 8 * g4 + 4 * h) >> 2];
-                    const float nh[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-#pragma unroll
-                        for (int nb = 0; nb < NB; ++nb)
-                            acc[mb][nb][4 * g4 + e] += nh[e];
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bone, acc[mb][nb], 0, 0, 0);
                 }
+            }
             float tsh[NB], ncth[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
@@ -1417,12 +1438,6 @@ __global__ __launch_bounds__(64) void ung_fallback_merge_kernel(FallbackParams F
 // ---------------------------------------------------------------------------
 // small kernels
 // ---------------------------------------------------------------------------
-// bf16 bits of x rounded to nearest, ties to even (finite x).
-__device__ __forceinline__ uint32_t bf16_rne(float x)
-{
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
 
 // Split base set for the MFMA pre-selection: x = hi + lo + r with hi = bf16(x) and
 // lo = bf16(x - hi) (x - hi is exact: both lie within a factor 2 of each other), so
