@@ -317,7 +317,9 @@ struct alignas(16) SelectSmem {
     uint32_t rowid[3][BC]; // candidate ids of tiles t%3 (ring: built one tile ahead; NONE = padding)
     float4 nhx[3][BC / 4]; // their -|x|^2/2 (-inf for padding rows), 4 rows per float4
     float qn[BQ];
-    float tau[2][2][BQ];   // [tile parity][candidate wave][query]: a wave's queue threshold
+    // [tile parity][candidate wave][query]: x = a wave's queue threshold, y = the larger
+    // m4-th entry of its two queues of the query
+    float2 tau[2][2][BQ];
 };
 static_assert(BQ == BC, "the epilogue staging addresses assume square panels");
 
@@ -340,7 +342,7 @@ struct alignas(16) SelectSmemQ {
     uint32_t rowid[3][BC];
     float4 nhx[3][BC / 4];
     float qn[BQ];
-    float tau[2][2][BQ];
+    float2 tau[2][2][BQ];
 };
 // flat float offsets inside SelectSmem::u.p
 constexpr int PANEL_X = 2 * BQ * LDSW; // start of xs relative to qs
@@ -623,6 +625,12 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     // thresholds may be shared between a query's queues only when one queue's LT
     // entries already cover the k results
     const bool share = P.k <= (uint32_t)LT;
+    // ranks of the counting bounds, fixed per queue length for the largest Lp it serves
+    // (LT = 8: Lp <= 12, 16: <= 20, 32: <= 80); a bound is used only if 4*M4 >= Lp+1
+    // (2*M2 >= Lp+1)
+    constexpr int M4 = LT == 8 ? 4 : LT == 16 ? 6 : 21;
+    constexpr int M2 = LT == 8 ? 7 : LT == 16 ? 11 : 0;
+    const bool use4 = 4u * M4 >= P.lp + 1u, use2 = M2 > 0 && 2u * M2 >= P.lp + 1u;
 
     // loader mapping: rows lr = (tid>>3) + RSTEP*m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
@@ -841,7 +849,13 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bone, acc[mb][nb], 0, 0, 0);
                 }
             }
-            float tsh[NB], ncth[NB];
+            //
+            // Counting bounds, valid for any k: the four queues' m4 best entries (4*m4 >=
+            // Lp+1) all lie at or below the largest of their m4-th entries, so a candidate
+            // at or above that value is not among the query's Lp+1 best; likewise the two
+            // queues of this wave with m2 (2*m2 >= Lp+1).  The other wave's value is from
+            // the previous tile: entries only decrease, so it bounds the current one.
+            float tsh[NB], ncth[NB], pm4[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 const int col = wn * QW + nb * 32 + r;
@@ -851,8 +865,16 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 if (share) {
                     t = fminf(t, partner);
                     if (tile > 0)
-                        t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col]);
+                        t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col].x);
                 }
+                const float o4 = use4 ? ld[nb][M4 - 1] : INFINITY;
+                pm4[nb] = fmaxf(o4, __shfl_xor(o4, 32));
+                if constexpr (M2 > 0) {
+                    const float o2 = use2 ? ld[nb][M2 - 1] : INFINITY;
+                    t = fminf(t, fmaxf(o2, __shfl_xor(o2, 32)));
+                }
+                if (tile > 0)
+                    t = fminf(t, fmaxf(pm4[nb], sm.tau[(tile - 1) & 1][wm ^ 1][col].y));
                 tsh[nb] = t;
                 ncth[nb] = -s_bound(t, qnv[nb]);
             }
@@ -957,11 +979,8 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     }
                 }
             } else {
-                // register-query layout: a thread owns 16 floats of the candidate panel it
-                // fills at the next step (buffer buf^1), so the two 16-candidate halves of
-                // a list are staged and inserted one after the other
-                float *const xsf = reinterpret_cast<float *>(&sm.u.p.xs[0][0][0]);
-                const int own0 = ((buf ^ 1) * BC + lr0) * LDSW + c4;
+                // register-query layout: no LDS room to stage a list, a round reads its
+                // element from the accumulators through a select tree
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
                     if (tile == 0) {
@@ -998,19 +1017,21 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                             }
                         }
                     } else {
+                        // element j of the list through a select tree over its 32
+                        // accumulator values (bit 4 of j: the half, bits 3..0: the entry)
+                        auto pick = [&](uint32_t j) -> float {
+                            float v[16];
 #pragma unroll
-                        for (int hv = 0; hv < 2; ++hv) {
+                            for (int i = 0; i < 16; ++i)
+                                v[i] = (j & 16u) ? acc[1][nb][i] : acc[0][nb][i];
 #pragma unroll
-                            for (int g4 = 0; g4 < 4; ++g4)
-                                *reinterpret_cast<float4 *>(&xsf[own0 + g4 * ROW32]) =
-                                    make_float4(acc[hv][nb][4 * g4], acc[hv][nb][4 * g4 + 1], acc[hv][nb][4 * g4 + 2],
-                                                acc[hv][nb][4 * g4 + 3]);
-                            auto staged = [&](uint32_t j) -> float & {
-                                const uint32_t i = j - 16u * (uint32_t)hv;
-                                return xsf[own0 + (int)(i >> 2) * ROW32 + (int)(i & 3u)];
-                            };
-                            rounds(nb, pend[nb] & (hv == 0 ? 0xFFFF0000u : 0x0000FFFFu), staged);
-                        }
+                            for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+                                for (int i = 0; i < w; ++i)
+                                    v[i] = (j & (uint32_t)w) ? v[i + w] : v[i];
+                            return v[0];
+                        };
+                        rounds(nb, pend[nb], pick);
                     }
                 }
             }
@@ -1020,8 +1041,8 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 const float t = fminf(tsh[nb], ld[nb][LT - 1]);
                 tfin[nb] = t;
                 const float pair_t = fminf(t, __shfl_xor(t, 32));
-                if (share && h == 0)
-                    sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
+                if (h == 0)
+                    sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = make_float2(pair_t, pm4[nb]);
             }
             ++tile;
             kc_state = 0;
@@ -2256,8 +2277,11 @@ int launch_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P,
 //    truncates each of its 17 operands by at most one ulp of the largest and rounds once
 //    gives <= 17u per MFMA over 3d/16 MFMAs, 3.19 d*u*1.0079 |x||q|.  In a: <= 1.61 d*u
 //    (|q|+R)^2
-//  * adding -fl(|x|^2)/2 (one rounding) and the final fma: <= 2.01 u (|q|+R)^2
-// Sum <= (1.61 d + 99.4) u (|q|+R)^2; the factor below keeps a margin.  Flushed bf16 or
+//  * adding -fl(|x|^2)/2 by one more MFMA whose three bf16 products sum exactly to that
+//    fp32 value: one rounding (measured), at most 4 operand truncations and one rounding
+//    in the fused-adder model above, <= 4.5 u max(|acc|, |x|^2/2) <= 2.25 u (|q|+R)^2;
+//    the final fma: <= 1.01 u (|q|+R)^2
+// Sum <= (1.61 d + 100.6) u (|q|+R)^2; the factor below keeps a margin.  Flushed bf16 or
 // fp32 subnormals add at most ~6d * 2^-126 absolute, covered by the 1e-30 term of
 // lower_bound_exact.
 double eps_coef_for(uint32_t d)
