@@ -315,11 +315,11 @@ struct alignas(16) SelectSmem {
         SelectRed r;
     } u;
     uint32_t rowid[3][BC]; // candidate ids of tiles t%3 (ring: built one tile ahead; NONE = padding)
-    float4 nhx[3][BC / 4]; // their -|x|^2/2 (-inf for padding rows), 4 rows per float4
+    // their -|x|^2/2 as the A words of the bias MFMA: bf16 terms hi | mid << 16, lo (padding
+    // rows: -inf, 0, 0)
+    uint2 nhx[3][BC];
     float qn[BQ];
-    // [tile parity][candidate wave][query]: x = a wave's queue threshold, y = the larger
-    // m4-th entry of its two queues of the query
-    float2 tau[2][2][BQ];
+    float tau[2][2][BQ];   // [tile parity][candidate wave][query]: a wave's queue threshold
 };
 static_assert(BQ == BC, "the epilogue staging addresses assume square panels");
 
@@ -340,9 +340,9 @@ struct alignas(16) SelectSmemQ {
         SelectRed r;
     } u;
     uint32_t rowid[3][BC];
-    float4 nhx[3][BC / 4];
+    uint2 nhx[3][BC];
     float qn[BQ];
-    float2 tau[2][2][BQ];
+    float tau[2][2][BQ];
 };
 // flat float offsets inside SelectSmem::u.p
 constexpr int PANEL_X = 2 * BQ * LDSW; // start of xs relative to qs
@@ -434,8 +434,16 @@ __device__ __forceinline__ float start_rowids(Smem &sm, int slot, RowCursor &cur
 template <class Smem>
 __device__ __forceinline__ void finish_rowids(Smem &sm, int slot, float nx, int tid)
 {
-    if (tid < BC)
-        reinterpret_cast<float *>(sm.nhx[slot])[tid] = -0.5f * nx; // -|x|^2/2 (exact scaling)
+    if (tid < BC) {
+        // -|x|^2/2 (exact scaling) split exactly into three bf16 terms
+        const float v = -0.5f * nx;
+        const uint32_t hi = bf16_rne(v);
+        const float r1 = v - __uint_as_float(hi << 16);
+        const uint32_t mid = bf16_rne(r1);
+        const uint32_t lo = bf16_rne(r1 - __uint_as_float(mid << 16));
+        const bool fin = v > -INFINITY;
+        sm.nhx[slot][tid] = make_uint2(hi | (fin ? mid << 16 : 0u), fin ? lo : 0u);
+    }
 }
 
 // Tile row (0..127) of a lane's j-th value of one query column, j = 16*mb + i of
@@ -625,12 +633,6 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     // thresholds may be shared between a query's queues only when one queue's LT
     // entries already cover the k results
     const bool share = P.k <= (uint32_t)LT;
-    // ranks of the counting bounds, fixed per queue length for the largest Lp it serves
-    // (LT = 8: Lp <= 12, 16: <= 20, 32: <= 80); a bound is used only if 4*M4 >= Lp+1
-    // (2*M2 >= Lp+1)
-    constexpr int M4 = LT == 8 ? 4 : LT == 16 ? 6 : 21;
-    constexpr int M2 = LT == 8 ? 7 : LT == 16 ? 11 : 0;
-    const bool use4 = 4u * M4 >= P.lp + 1u, use2 = M2 > 0 && 2u * M2 >= P.lp + 1u;
 
     // loader mapping: rows lr = (tid>>3) + RSTEP*m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
@@ -830,32 +832,19 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
             // The three products sum exactly to the fp32 value, so the MFMA performs the
             // one rounded fp32 addition acc + (-|x|^2/2).
             {
-                const float *const nhf = reinterpret_cast<const float *>(&sm.nhx[slot][0]);
                 const bf16x8 bone = __builtin_bit_cast(
                     bf16x8, make_uint4(h == 0 ? 0x3F803F80u : 0u, h == 0 ? 0x00003F80u : 0u, 0u, 0u));
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb) {
-                    const float v = nhf[wm * 64 + 32 * mb + r];
-                    const uint32_t hi = bf16_rne(v);
-                    const float r1 = v - __uint_as_float(hi << 16);
-                    const uint32_t mid = bf16_rne(r1);
-                    const uint32_t lo = bf16_rne(r1 - __uint_as_float(mid << 16));
-                    const bool tail = h == 0 && v > -INFINITY;
-                    const uint32_t w0 = h == 0 ? (hi | (tail ? mid << 16 : 0u)) : 0u;
-                    const uint32_t w1 = tail ? lo : 0u;
-                    const bf16x8 abias = __builtin_bit_cast(bf16x8, make_uint4(w0, w1, 0u, 0u));
+                    const uint2 w = sm.nhx[slot][wm * 64 + 32 * mb + r];
+                    const bf16x8 abias =
+                        __builtin_bit_cast(bf16x8, make_uint4(h == 0 ? w.x : 0u, h == 0 ? w.y : 0u, 0u, 0u));
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bone, acc[mb][nb], 0, 0, 0);
                 }
             }
-            //
-            // Counting bounds, valid for any k: the four queues' m4 best entries (4*m4 >=
-            // Lp+1) all lie at or below the largest of their m4-th entries, so a candidate
-            // at or above that value is not among the query's Lp+1 best; likewise the two
-            // queues of this wave with m2 (2*m2 >= Lp+1).  The other wave's value is from
-            // the previous tile: entries only decrease, so it bounds the current one.
-            float tsh[NB], ncth[NB], pm4[NB];
+            float tsh[NB], ncth[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 const int col = wn * QW + nb * 32 + r;
@@ -865,16 +854,8 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 if (share) {
                     t = fminf(t, partner);
                     if (tile > 0)
-                        t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col].x);
+                        t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col]);
                 }
-                const float o4 = use4 ? ld[nb][M4 - 1] : INFINITY;
-                pm4[nb] = fmaxf(o4, __shfl_xor(o4, 32));
-                if constexpr (M2 > 0) {
-                    const float o2 = use2 ? ld[nb][M2 - 1] : INFINITY;
-                    t = fminf(t, fmaxf(o2, __shfl_xor(o2, 32)));
-                }
-                if (tile > 0)
-                    t = fminf(t, fmaxf(pm4[nb], sm.tau[(tile - 1) & 1][wm ^ 1][col].y));
                 tsh[nb] = t;
                 ncth[nb] = -s_bound(t, qnv[nb]);
             }
@@ -1041,8 +1022,8 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 const float t = fminf(tsh[nb], ld[nb][LT - 1]);
                 tfin[nb] = t;
                 const float pair_t = fminf(t, __shfl_xor(t, 32));
-                if (h == 0)
-                    sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = make_float2(pair_t, pm4[nb]);
+                if (share && h == 0)
+                    sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
             }
             ++tile;
             kc_state = 0;
