@@ -219,7 +219,8 @@ def main():
         roofline = {"bound": "mfma", "achieved": round(mfma_tflops, 3), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(mfma_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic}
     roofline.update({
-        "kernel": "ung_select_kernel<8,1,false> (cross edges, one launch per step)",
+        "kernel": ("ung_select_kernel<8,1,false,2,true> (cross edges, register-query layout, one launch per step)"
+                   if dp == 128 else "ung_select_kernel<8,1,false,2,false> (cross edges, one launch per step)"),
         "avg_launch_ms": round(sel_cross_ms, 4),
         "alg_bytes_per_launch": alg_bytes, "hbm_floor_ms": round(hbm_floor_ms, 3),
         "mfma_bf16_flops_per_launch": mfma_flops, "mfma_floor_ms": round(mfma_floor_ms, 3),
