@@ -587,7 +587,7 @@ template <int LT, int MODE, bool EXCL, int NB, bool QR>
 __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_select_kernel(SelectParams P)
 {
     static_assert(NB == 1 || NB == 2, "one or two query columns per lane");
-    static_assert(!QR || (NB == 2 && LT == 8 && MODE == LOAD_BUF32), "register-query layout: NB = 2, LT = 8, 32-bit loads");
+    static_assert(!QR || (NB == 2 && LT == 8), "register-query layout: NB = 2, LT = 8");
     constexpr int NTH = select_threads<NB>();
     constexpr int WN = 4 / NB;         // query waves
     constexpr int QW = 32 * NB;        // query columns per wave
@@ -658,21 +658,25 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     // the item's queries (float4 column 4*chunk + c of row q) into LDS
     [[maybe_unused]] bf16x8 bhr[2 * QR_NK][NB];
     if constexpr (QR) {
+        // 32-bit loads: rows of the whole split set; wide loads: rows of the item's queries
+        // (q0 = 0 in that buffer, zeros past its qcnt rows)
+        const __amdgpu_buffer_rsrc_t qr_res = MODE == LOAD_BUF32 ? xres : qres;
+        const uint32_t qr0 = MODE == LOAD_BUF32 ? q0 : 0u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const uint32_t row = q0 + (uint32_t)(wn * QW + 32 * nb + r);
+            const uint32_t row = qr0 + (uint32_t)(wn * QW + 32 * nb + r);
 #pragma unroll
             for (int kb = 0; kb < 2 * QR_NK; ++kb)
                 bhr[kb][nb] = __builtin_bit_cast(
                     bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                xres, (row * dp + (uint32_t)((kb >> 1) * KC + (2 * (kb & 1) + h) * 4)) * 4u, 0, 0));
+                                qr_res, (row * dp + (uint32_t)((kb >> 1) * KC + (2 * (kb & 1) + h) * 4)) * 4u, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < BQ * QR_NK * 4 / NTH; ++i) {
             const int idx = tid + NTH * i;
             const int q = idx >> 4, f = idx & 15; // f = 4*chunk + float4 column of the low words
-            const uint32_t off = ((q0 + (uint32_t)q) * dp + (uint32_t)((f >> 2) * KC + 16 + (f & 3) * 4)) * 4u;
-            sm.u.p.qlo[q][f] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
+            const uint32_t off = ((qr0 + (uint32_t)q) * dp + (uint32_t)((f >> 2) * KC + 16 + (f & 3) * 4)) * 4u;
+            sm.u.p.qlo[q][f] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qr_res, off, 0, 0));
         }
     }
 
@@ -711,7 +715,8 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
             } else {
-                rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff, kc * 4u + m * qrow_step, 0));
+                if constexpr (!QR)
+                    rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, *reinterpret_cast<const u32x4 *>(xrow[m] + kc));
             }
         }
@@ -2223,13 +2228,17 @@ int launch_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P,
         // queues longer than 8 take the one-column-per-lane layout (two waves per SIMD)
         constexpr int NB = LT <= 8 ? 2 : 1;
         const dim3 g(n), b(select_threads<NB>());
-        // two columns per lane, dp = 128 and 32-bit loads: the register-query layout
-        const bool qr = NB == 2 && mode == LOAD_BUF32 && ctx->dp == (uint32_t)(QR_NK * KC) && ctx->qreg;
+        // two columns per lane and dp = 128: the register-query layout
+        const bool qr = NB == 2 && ctx->dp == (uint32_t)(QR_NK * KC) && ctx->qreg;
         if constexpr (NB == 2) {
-            if (qr && excl)
+            if (qr && mode == LOAD_BUF32 && excl)
                 hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, true, NB, true>), g, b, 0, stream, Q);
-            else if (qr)
+            else if (qr && mode == LOAD_BUF32)
                 hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_BUF32, false, NB, true>), g, b, 0, stream, Q);
+            else if (qr && excl)
+                hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, true, NB, true>), g, b, 0, stream, Q);
+            else if (qr)
+                hipLaunchKernelGGL((ung_select_kernel<LT, LOAD_WIDE, false, NB, true>), g, b, 0, stream, Q);
         }
         if (qr)
             ; // launched above

@@ -106,7 +106,7 @@ def test_wide_cross(wide_ctx, oracle, dim, k, seed):
     _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, f"wide dim={dim} k={k}")
 
 
-@pytest.mark.parametrize("n,list_k,dim", [(129, 32, 128), (700, 32, 384), (300, 8, 20)])
+@pytest.mark.parametrize("n,list_k,dim", [(129, 32, 128), (700, 32, 384), (300, 8, 20), (300, 6, 128)])
 def test_wide_intra(wide_ctx, oracle, n, list_k, dim):
     print(f"wide intra n={n} k={list_k} dim={dim}", flush=True)
     rng = np.random.default_rng(n + dim)
@@ -116,6 +116,38 @@ def test_wide_intra(wide_ctx, oracle, n, list_k, dim):
     ids, dist, _ = wide_ctx.group_knn([3], [n], list_k)
     oi, od = oracle.intra_exact(X, 3, n, list_k)
     _assert_rows_equal(ids, dist, None, oi, od, None, f"wide intra n={n}")
+
+
+@pytest.fixture(scope="module")
+def panel_ctx():
+    c = _ctx_with_env("UNG_HIP_NO_QREG", "1")
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("dim,k,seed", [(128, 6, 41), (128, 8, 42)])
+def test_panel_layout_cross(panel_ctx, oracle, dim, k, seed):
+    """dp = 128 with the query panel restaged every step (the layout every other dp uses)."""
+    print(f"panel cross dim={dim} k={k}", flush=True)
+    rng = np.random.default_rng(seed)
+    X, gb, op, oi = _two_level_problem(rng, [1, 3, 130, 300, 7], [4, 200, 2, 129, 5], dim, dup=True)
+    panel_ctx.prepare_vectors(X)
+    ids, dist, size, _ = panel_ctx.cross_topk(gb, op, oi, k)
+    ip, ii = F.in_neighbors(op, oi)
+    o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, k)
+    _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, f"panel dim={dim} k={k}")
+
+
+@pytest.mark.parametrize("n,list_k", [(300, 6), (1000, 8)])
+def test_panel_layout_intra(panel_ctx, oracle, n, list_k):
+    print(f"panel intra n={n} k={list_k}", flush=True)
+    rng = np.random.default_rng(n + 128)
+    X = rng.standard_normal((n + 7, 128)).astype(np.float32)
+    X[5] = X[3]
+    panel_ctx.prepare_vectors(X)
+    ids, dist, _ = panel_ctx.group_knn([3], [n], list_k)
+    oi, od = oracle.intra_exact(X, 3, n, list_k)
+    _assert_rows_equal(ids, dist, None, oi, od, None, f"panel intra n={n}")
 
 
 def _checker(oracle):
