@@ -2305,6 +2305,9 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
         const size_t bj = pl.jobs.size() * sizeof(Job), bi = pl.items.size() * sizeof(Item);
         const size_t bm = pl.mitems.size() * sizeof(MergeItem), bs = pl.seg_start.size() * sizeof(uint32_t);
         const size_t oj = 0, oi = al(bj), om = oi + al(bi), os = om + al(bm), ov = os + al(bs);
+        // the previous call's uploads from this staging buffer have completed (its select
+        // start event follows them on the stream)
+        HIPCHECK(hipEventSynchronize(ws.ev[0]));
         if ((rc = ws.stage.ensure(ov + al(bs))))
             return rc;
         char *hs = static_cast<char *>(ws.stage.p);
@@ -2329,7 +2332,6 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
         HIPCHECK(hipMemcpyAsync(ws.seg_start.p, hs + os, bs, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(ws.seg_vend.p, hs + ov, bs, hipMemcpyHostToDevice, ws.stream));
     }
-    HIPCHECK(hipStreamSynchronize(ws.stream)); // the pinned staging is reused by the next call
     if (st)
         st->h2d_ms += ms_since(t_h2d);
     if (pl.jobs.empty())
@@ -2515,6 +2517,12 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
             return UNG_HIP_EINVAL;
         }
     }
+    // upper bounds of the list sizes: no reallocation while planning
+    pl.seg_start.reserve(out_ptr[G + 1]);
+    pl.seg_vend.reserve(out_ptr[G + 1]);
+    pl.jobs.reserve(G);
+    pl.mitems.reserve(ctx->N / MERGE_ROWS + G);
+    pl.pitems.reserve(ctx->N / MERGE_Q + G);
     for (uint32_t c = 1; c <= G; ++c) {
         const uint32_t qn = group_begin[c + 1] - group_begin[c];
         if (qn == 0 || out_ptr[c + 1] == out_ptr[c])
@@ -2638,14 +2646,15 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         return rc;
     if (st)
         st->plan_ms += ms_since(t0);
+    if ((rc = cross_prepare_result(ctx, k)) || (rc = plan_launch(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
+        return rc;
+    // the group call is planned while the cross kernels run
     ctx->intra_stats = ung_hip_stats{};
     ctx->intra_t0 = clk::now();
     ctx->intra_plan = Plan{};
     if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, ctx->intra_plan)))
         return rc;
     ctx->intra_stats.plan_ms += ms_since(ctx->intra_t0);
-    if ((rc = cross_prepare_result(ctx, k)) || (rc = plan_launch(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
-        return rc;
     // from here the group call is in flight on the second workspace until intra_end
     ctx->intra_list_k = list_k;
     ctx->intra_pending = true;

@@ -327,6 +327,20 @@ def test_cross_intra_overlapped_equals_sequential(ctx, oracle):
         for a, w in zip(got_add[:3], want_add[:3]):
             assert np.array_equal(a, w)
         assert np.array_equal(check_ids, g_ids) and np.array_equal(check_dist, g_dist)
+    # an invalid group list is refused (the cross kernels it already started finish on
+    # their own); the next overlapped call gives the same rows
+    bad_n = n.copy()
+    bad_n[0] = 0
+    with pytest.raises(F.UngHipError):
+        ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, 6, b, bad_n, 32)
+    with pytest.raises(F.UngHipError):
+        ctx.intra_end()
+    ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, 6, b, n, 32)
+    ids, dist, size, _ = ctx.download_cross(st.base.shape[0], 6)
+    ctx.intra_end()
+    check_ids, check_dist, _ = ctx.download_group(g_ids.shape[0], 32)
+    assert np.array_equal(ids, c_ids) and np.array_equal(dist, c_dist) and np.array_equal(size, c_size)
+    assert np.array_equal(check_ids, g_ids) and np.array_equal(check_dist, g_dist)
     # the cross rows also equal the oracle's on a sample (the sequential call is pinned elsewhere)
     pg = st.new_vec_id_to_group_id
     q = np.arange(0, st.base.shape[0], 97, dtype=np.uint32)
