@@ -595,6 +595,12 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     constexpr int LM = BQ / RSTEP;     // rows per thread and panel
     __shared__ typename std::conditional<QR, SelectSmemQ, SelectSmem>::type sm;
     __shared__ typename std::conditional<NB == 1, SelectStage, NoStage>::type stage;
+    // long queues: [tile parity][candidate wave][query] the larger m4-th entry of a wave's
+    // two queues of the query
+    struct Tau4 {
+        float v[2][2][BQ];
+    };
+    __shared__ typename std::conditional<(LT >= 16), Tau4, NoStage>::type tau4;
     __shared__ uint32_t item_slot;
     const uint32_t logical = take_item(P.item_ctr, &item_slot);
     if (logical >= P.n_items)
@@ -633,6 +639,8 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     // thresholds may be shared between a query's queues only when one queue's LT
     // entries already cover the k results
     const bool share = P.k <= (uint32_t)LT;
+    // counting bound of the long queues (LT >= 16): 4*m4 >= Lp+1 (Lp = P.lp < 4*LT)
+    [[maybe_unused]] const uint32_t m4 = (P.lp + 4u) / 4u;
 
     // loader mapping: rows lr = (tid>>3) + RSTEP*m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
@@ -849,7 +857,14 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bone, acc[mb][nb], 0, 0, 0);
                 }
             }
+            //
+            // Long queues (LT >= 16) also apply a counting bound, valid for any k: the
+            // query's four queues hold m4 entries each at or below the largest of their
+            // m4-th entries (4*m4 >= Lp+1 entries in all), so a candidate at or above that
+            // value is not among the query's Lp+1 best.  The other wave's value is from the
+            // previous tile: entries only decrease, so it bounds the current one.
             float tsh[NB], ncth[NB];
+            [[maybe_unused]] float pm4[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 const int col = wn * QW + nb * 32 + r;
@@ -860,6 +875,15 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     t = fminf(t, partner);
                     if (tile > 0)
                         t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col]);
+                }
+                if constexpr (LT >= 16) {
+                    float o4 = INFINITY;
+#pragma unroll
+                    for (int j = 0; j < LT; ++j)
+                        o4 = (uint32_t)j + 1u == m4 ? ld[nb][j] : o4;
+                    pm4[nb] = fmaxf(o4, __shfl_xor(o4, 32));
+                    if (tile > 0)
+                        t = fminf(t, fmaxf(pm4[nb], tau4.v[(tile - 1) & 1][wm ^ 1][col]));
                 }
                 tsh[nb] = t;
                 ncth[nb] = -s_bound(t, qnv[nb]);
@@ -1029,6 +1053,9 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 const float pair_t = fminf(t, __shfl_xor(t, 32));
                 if (share && h == 0)
                     sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
+                if constexpr (LT >= 16)
+                    if (h == 0)
+                        tau4.v[tile & 1][wm][wn * QW + nb * 32 + r] = pm4[nb];
             }
             ++tile;
             kc_state = 0;
