@@ -559,6 +559,49 @@ __device__ __forceinline__ void best_of_32(float (&d)[32], uint32_t (&id)[32], f
     }
 }
 
+// Ascending bitonic sort of 32 (dist, id) entries (240 compare-exchanges).
+__device__ __forceinline__ void sort32(float (&d)[32], uint32_t (&id)[32])
+{
+#pragma unroll
+    for (int k = 2; k <= 32; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int l = i ^ j;
+                if (l > i) {
+                    if ((i & k) == 0)
+                        cas(d, id, i, l);
+                    else
+                        cas(d, id, l, i);
+                }
+            }
+}
+
+// The 32 smallest of an ascending queue of 32 and 32 new entries, ascending, into the
+// queue: the new entries sorted, a half cleaner (queue[i] vs new[31-i]) leaves the 32
+// smallest as a bitonic run, a bitonic merge sorts it (352 compare-exchanges in all,
+// whatever the number of entries that enter).
+__device__ __forceinline__ void merge_into_queue32(float (&d)[32], uint32_t (&id)[32], float (&ld)[32],
+                                                   uint32_t (&li)[32])
+{
+    sort32(d, id);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const uint32_t m = (uint32_t)((int32_t)__float_as_uint(d[31 - i] - ld[i]) >> 31);
+        ld[i] = __uint_as_float(bitsel(m, __float_as_uint(d[31 - i]), __float_as_uint(ld[i])));
+        li[i] = bitsel(m, id[31 - i], li[i]);
+    }
+#pragma unroll
+    for (int j = 16; j > 0; j >>= 1)
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int l = i ^ j;
+            if (l > i)
+                cas(ld, li, i, l);
+        }
+}
+
 // Operand loads from the split base set (rows of dp words, every chunk whole):
 //   LOAD_BUF32 : split set smaller than 4 GiB -- buffer loads with 32-bit byte offsets;
 //                the k-chunk advances a scalar offset, so the main loop spends no vector
@@ -920,7 +963,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
             // body is branch-free (an idle lane inserts +inf, which changes nothing) and the
             // round count is the wave's largest pending count (binary search on ballots:
             // wave-uniform, no cross-lane data movement).  staged(j) is element j's value.
-            auto rounds = [&](int nb, uint32_t m, auto &&staged) __attribute__((always_inline)) {
+            auto round_count = [&](uint32_t m) __attribute__((always_inline)) -> uint32_t {
                 const uint32_t np = (uint32_t)__popc(m);
                 uint32_t nr = 0;
 #pragma unroll
@@ -929,6 +972,9 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     if (__ballot(np >= c))
                         nr = c;
                 }
+                return nr;
+            };
+            auto rounds = [&](int nb, uint32_t m, uint32_t nr, auto &&staged) __attribute__((always_inline)) {
                 for (uint32_t rr = 0; rr < nr; ++rr) {
                     const uint32_t j = (uint32_t)__builtin_clz(m | 1u);
                     const bool act = m != 0u;
@@ -985,7 +1031,30 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                         }
                         best_of_32<LT>(dv, iv, ld[nb], li[nb]);
                     } else {
-                        rounds(nb, pend[nb], staged);
+                        const uint32_t nr = round_count(pend[nb]);
+                        bool merged = false;
+                        if constexpr (LT == 32) {
+                            // an early tile of a long queue: more than ~12 rounds (about 175
+                            // instructions each) cost more than merging the tile's 32 entries
+                            // with a sorting network
+                            if (nr > 12u) {
+                                float dv[32];
+                                uint32_t iv[32];
+#pragma unroll
+                                for (int g = 0; g < 8; ++g) {
+                                    const uint4 ids =
+                                        *reinterpret_cast<const uint4 *>(&sm.rowid[slot][tile_row(wm, h, 4u * g)]);
+                                    const uint32_t idg[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+                                    for (int e = 0; e < 4; ++e)
+                                        entry(nb, 4 * g + e, idg[e], dv[4 * g + e], iv[4 * g + e]);
+                                }
+                                merge_into_queue32(dv, iv, ld[nb], li[nb]);
+                                merged = true;
+                            }
+                        }
+                        if (!merged)
+                            rounds(nb, pend[nb], nr, staged);
                     }
                 }
             } else {
@@ -1041,7 +1110,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                                     v[i] = (j & (uint32_t)w) ? v[i + w] : v[i];
                             return v[0];
                         };
-                        rounds(nb, pend[nb], pick);
+                        rounds(nb, pend[nb], round_count(pend[nb]), pick);
                     }
                 }
             }
