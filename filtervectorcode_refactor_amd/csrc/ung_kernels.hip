@@ -42,7 +42,7 @@ constexpr int BC = 128;          // candidates per tile (rows of the MFMA tiles)
 constexpr int KC = 32;           // k-chunk staged in LDS (dimensions)
 constexpr int LDSW = KC + 4;     // padded LDS row stride (32-bit words; a chunk row is 32 words)
 constexpr int NTHREADS = 256;    // 4 waves: 2 (candidate halves) x 2 (query halves)
-constexpr uint32_t SPLIT_V = 16384; // candidates per work item (raised so a job has <= 64 splits)
+constexpr uint32_t SPLIT_V = 32768; // candidates per work item (raised so a job has <= 64 splits)
 constexpr uint32_t MAX_SPLITS = 64; // one wave lane per split in the merge
 constexpr uint32_t MERGE_ROWS = 4;  // result rows (one wave each) per merge block
 constexpr uint32_t MERGE_Q = 256;   // rows per packing block

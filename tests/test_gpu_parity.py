@@ -128,14 +128,15 @@ def test_cross_edge_cases(ctx, oracle, dim, k, seed):
 
 
 def test_cross_multi_split(ctx, oracle):
-    """Unions above one work item's candidate split (16384) are merged on device."""
+    """Unions above one work item's candidate split (32768) are merged on device."""
     rng = np.random.default_rng(11)
-    X, gb, op, oi = _two_level_problem(rng, [300, 5], [9000, 12000, 3], 128)
+    X, gb, op, oi = _two_level_problem(rng, [300, 5], [20000, 15000, 3], 128)
     op = np.array([0, 0, 3, 6, 6, 6, 6], np.uint32)
     oi = np.array([3, 4, 5, 3, 4, 5], np.uint32)
     ctx.prepare_vectors(X)
     ids, dist, size, stats = ctx.cross_topk(gb, op, oi, 6)
     _say(f"multi split stats {stats}")
+    assert stats["work_items"] > 4  # 4 query blocks, each over more than one split
     ip, ii = F.in_neighbors(op, oi)
     o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, 6)
     _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, "multi split")
