@@ -1239,6 +1239,7 @@ struct MergeParams {
 // certificate  T_k < lower bound of every candidate left out.
 __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams M)
 {
+    __shared__ uint32_t mrank[MERGE_ROWS][128]; // a wave's candidates in rank order
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const MergeItem mi = M.mitems[blockIdx.x];
     if ((uint32_t)w >= mi.q_cnt)
@@ -1259,6 +1260,69 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
             if ((uint32_t)(64 * h + lane) < Lp)
                 ci[h] = M.part_ids[prow * Lp + 64 * h + lane];
         B = M.part_bound[prow];
+    } else if (S * Lp <= 128u) {
+        // all S*Lp entries in the wave (two per lane): each entry's rank under (dist, id,
+        // entry index) by comparing with every other one, no dependent loads; the entry of
+        // rank t goes to lane t % 64, slot t / 64, the one of rank Lp is the first left out
+        const uint32_t n = S * Lp;
+        float ed[2];
+        uint32_t eid[2];
+        float bnd = INFINITY;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t e = 64u * (uint32_t)h + (uint32_t)lane;
+            ed[h] = INFINITY;
+            eid[h] = NONE;
+            if (e < n) {
+                const uint32_t sp = e / Lp, pos = e - sp * Lp;
+                const size_t prow = (size_t)jb.part_base + (size_t)sp * jb.q_count + ql;
+                ed[h] = M.part_dist[prow * Lp + pos];
+                eid[h] = M.part_ids[prow * Lp + pos];
+            }
+        }
+        if ((uint32_t)lane < S)
+            bnd = M.part_bound[(size_t)jb.part_base + (size_t)lane * jb.q_count + ql];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            bnd = fminf(bnd, __shfl_xor(bnd, off));
+        uint32_t rk[2] = {0u, 0u};
+        if (n <= 64u) {
+            for (uint32_t f = 0; f < n; ++f) {
+                const float df = __shfl(ed[0], (int)f);
+                const uint32_t idf = __shfl(eid[0], (int)f);
+                rk[0] += (df < ed[0] || (df == ed[0] && (idf < eid[0] || (idf == eid[0] && f < (uint32_t)lane)))) ? 1u : 0u;
+            }
+        } else {
+            for (uint32_t f = 0; f < n; ++f) {
+                const int src = (int)(f & 63u);
+                const float df = f < 64u ? __shfl(ed[0], src) : __shfl(ed[1], src);
+                const uint32_t idf = f < 64u ? __shfl(eid[0], src) : __shfl(eid[1], src);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t me = 64u * (uint32_t)h + (uint32_t)lane;
+                    rk[h] += (df < ed[h] || (df == ed[h] && (idf < eid[h] || (idf == eid[h] && f < me)))) ? 1u : 0u;
+                }
+            }
+        }
+        // scatter through this wave's LDS row: every rank below n is held by one entry
+        float a_next = INFINITY;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool in = 64u * (uint32_t)h + (uint32_t)lane < n;
+            if (in && rk[h] < Lp)
+                mrank[w][rk[h]] = eid[h];
+            if (in && rk[h] == Lp)
+                a_next = ed[h];
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            if (64u * (uint32_t)h + (uint32_t)lane < Lp)
+                ci[h] = mrank[w][64 * h + lane];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            a_next = fminf(a_next, __shfl_xor(a_next, off));
+        B = fminf(bnd, a_next);
     } else {
         size_t prow = 0;
         uint32_t pos = 0;
