@@ -2180,8 +2180,8 @@ struct HostBuf {
 struct Plan {
     std::vector<Job> jobs;
     std::vector<Item> items;
-    std::vector<MergeItem> mitems; // merge: MERGE_ROWS rows per block
-    std::vector<MergeItem> pitems; // packing: MERGE_Q rows per block
+    uint64_t n_mitems = 0;         // merge: MERGE_ROWS rows per block (written at launch)
+    std::vector<MergeItem> pitems; // packing: MERGE_Q rows per block (group plans)
     std::vector<uint32_t> seg_start, seg_vend;
     uint64_t part_rows = 0;
     uint64_t pairs = 0;
@@ -2214,7 +2214,9 @@ namespace {
 // the cross-edge call and the additional edges use the first.
 struct Workspace {
     hipStream_t stream = nullptr;
+    hipStream_t upload = nullptr; // merge-item uploads, beside the select kernel
     hipEvent_t ev[4] = {};
+    hipEvent_t ev_up = nullptr;   // merge items uploaded
     DevBuf<Job> jobs;
     DevBuf<Item> items;
     DevBuf<MergeItem> mitems;
@@ -2333,19 +2335,28 @@ void add_items_for_job(Plan &pl, uint32_t job_index)
             pl.padded += (uint64_t)BQ * (uint64_t)(((it.v_end - it.v_begin) + BC - 1) / BC * BC);
         }
     }
-    for (uint32_t qo = 0; qo < jb.q_count; qo += MERGE_ROWS) {
-        MergeItem mi{};
-        mi.job = job_index;
-        mi.q_off = qo;
-        mi.q_cnt = std::min<uint32_t>(MERGE_ROWS, jb.q_count - qo);
-        pl.mitems.push_back(mi);
+    pl.n_mitems += (jb.q_count + MERGE_ROWS - 1) / MERGE_ROWS;
+}
+
+// Merge items (MERGE_ROWS result rows of one job each) of a plan, written to `out`
+// (pl.n_mitems entries).
+void write_merge_items(const Plan &pl, MergeItem *out)
+{
+    size_t n = 0;
+    for (uint32_t j = 0; j < (uint32_t)pl.jobs.size(); ++j) {
+        const uint32_t qc = pl.jobs[j].q_count;
+        for (uint32_t qo = 0; qo < qc; qo += MERGE_ROWS)
+            out[n++] = MergeItem{j, qo, std::min<uint32_t>(MERGE_ROWS, qc - qo), 0u};
     }
-    for (uint32_t qo = 0; qo < jb.q_count; qo += MERGE_Q) {
-        MergeItem mi{};
-        mi.job = job_index;
-        mi.q_off = qo;
-        mi.q_cnt = std::min<uint32_t>(MERGE_Q, jb.q_count - qo);
-        pl.pitems.push_back(mi);
+}
+
+// Packing items (MERGE_Q rows of one job each) of a group plan.
+void add_pack_items(Plan &pl)
+{
+    for (uint32_t j = 0; j < (uint32_t)pl.jobs.size(); ++j) {
+        const uint32_t qc = pl.jobs[j].q_count;
+        for (uint32_t qo = 0; qo < qc; qo += MERGE_Q)
+            pl.pitems.push_back(MergeItem{j, qo, std::min<uint32_t>(MERGE_Q, qc - qo), 0u});
     }
 }
 
@@ -2451,7 +2462,7 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     const uint32_t lp = pick_lp(k, lt);
     const auto t_h2d = clk::now();
     if ((rc = ws.jobs.ensure(pl.jobs.size())) || (rc = ws.items.ensure(pl.items.size())) ||
-        (rc = ws.mitems.ensure(pl.mitems.size())) || (rc = ws.seg_start.ensure(pl.seg_start.size())) ||
+        (rc = ws.mitems.ensure(pl.n_mitems)) || (rc = ws.seg_start.ensure(pl.seg_start.size())) ||
         (rc = ws.seg_vend.ensure(pl.seg_vend.size())) ||
         (rc = ws.part_ids.ensure(pl.part_rows * lp)) || (rc = ws.part_dist.ensure(pl.part_rows * lp)) ||
         (rc = ws.part_bound.ensure(pl.part_rows)) || (rc = ws.flag_count.ensure(2)) ||
@@ -2460,19 +2471,21 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     // select items in order of decreasing cost (candidate tiles); the stable sort keeps
     // the query blocks of one split next to each other
     // (a counting sort by tile count: stable, linear in the item count)
+    // staging layout: jobs | items | seg_start | seg_vend | merge items (written after the
+    // select kernel is enqueued, so building and uploading them overlaps it)
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t bj = pl.jobs.size() * sizeof(Job), bi = pl.items.size() * sizeof(Item);
+    const size_t bm = pl.n_mitems * sizeof(MergeItem), bs = pl.seg_start.size() * sizeof(uint32_t);
+    const size_t oj = 0, oi = al(bj), os = oi + al(bi), ov = os + al(bs), om = ov + al(bs);
+    char *hs = nullptr;
     if (!pl.jobs.empty()) {
-        auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-        const size_t bj = pl.jobs.size() * sizeof(Job), bi = pl.items.size() * sizeof(Item);
-        const size_t bm = pl.mitems.size() * sizeof(MergeItem), bs = pl.seg_start.size() * sizeof(uint32_t);
-        const size_t oj = 0, oi = al(bj), om = oi + al(bi), os = om + al(bm), ov = os + al(bs);
-        // the previous call's uploads from this staging buffer have completed (its select
-        // start event follows them on the stream)
-        HIPCHECK(hipEventSynchronize(ws.ev[0]));
-        if ((rc = ws.stage.ensure(ov + al(bs))))
+        // the previous call's uploads from this staging buffer have completed (its merge
+        // launch event follows them on the stream)
+        HIPCHECK(hipEventSynchronize(ws.ev[2]));
+        if ((rc = ws.stage.ensure(om + al(bm))))
             return rc;
-        char *hs = static_cast<char *>(ws.stage.p);
+        hs = static_cast<char *>(ws.stage.p);
         std::memcpy(hs + oj, pl.jobs.data(), bj);
-        std::memcpy(hs + om, pl.mitems.data(), bm);
         std::memcpy(hs + os, pl.seg_start.data(), bs);
         std::memcpy(hs + ov, pl.seg_vend.data(), bs);
         uint32_t max_t = 0;
@@ -2488,7 +2501,6 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
             sorted[start[max_t - (it.v_end - it.v_begin + BC - 1) / BC]++] = it;
         HIPCHECK(hipMemcpyAsync(ws.jobs.p, hs + oj, bj, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(ws.items.p, hs + oi, bi, hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.mitems.p, hs + om, bm, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(ws.seg_start.p, hs + os, bs, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(ws.seg_vend.p, hs + ov, bs, hipMemcpyHostToDevice, ws.stream));
     }
@@ -2534,6 +2546,15 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
         return rc;
     HIPCHECK(hipEventRecord(ws.ev[1], ws.stream));
 
+    // merge items, built and uploaded (on the upload stream) while the select kernel runs
+    const auto t_mi = clk::now();
+    write_merge_items(pl, reinterpret_cast<MergeItem *>(hs + om));
+    HIPCHECK(hipMemcpyAsync(ws.mitems.p, hs + om, bm, hipMemcpyHostToDevice, ws.upload));
+    HIPCHECK(hipEventRecord(ws.ev_up, ws.upload));
+    HIPCHECK(hipStreamWaitEvent(ws.stream, ws.ev_up, 0));
+    if (st)
+        st->h2d_ms += ms_since(t_mi);
+
     MergeParams M{};
     M.X = ctx->X;
     M.xn = ctx->xn;
@@ -2553,7 +2574,7 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     M.out_size = res.size.p;
     M.flag_count = ws.flag_count.p;
     M.flagged = ws.flagged.p;
-    const uint32_t n_m = (uint32_t)pl.mitems.size();
+    const uint32_t n_m = (uint32_t)pl.n_mitems;
     for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
         MergeParams Mc = M;
         Mc.mitems = M.mitems + off;
@@ -2681,8 +2702,6 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
     pl.seg_start.reserve(out_ptr[G + 1]);
     pl.seg_vend.reserve(out_ptr[G + 1]);
     pl.jobs.reserve(G);
-    pl.mitems.reserve(ctx->N / MERGE_ROWS + G);
-    pl.pitems.reserve(ctx->N / MERGE_Q + G);
     for (uint32_t c = 1; c <= G; ++c) {
         const uint32_t qn = group_begin[c + 1] - group_begin[c];
         if (qn == 0 || out_ptr[c + 1] == out_ptr[c])
@@ -2915,6 +2934,7 @@ int build_group_plan(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_be
         pl.jobs.push_back(jb);
         add_items_for_job(pl, (uint32_t)pl.jobs.size() - 1);
     }
+    add_pack_items(pl);
     return UNG_HIP_OK;
 }
 
@@ -3259,8 +3279,12 @@ int ung_hip_create(int device, ung_hip_ctx **out)
         ctx->eps_scale = v >= 1.0 ? v : 1.0; // a smaller bound would not be an error bound
     }
     hipError_t e = hipSuccess;
-    for (auto &w : ctx->ws) { // both streams at the default priority
+    for (auto &w : ctx->ws) { // all streams at the default priority
         e = hipStreamCreateWithFlags(&w.stream, hipStreamNonBlocking);
+        if (e == hipSuccess)
+            e = hipStreamCreateWithFlags(&w.upload, hipStreamNonBlocking);
+        if (e == hipSuccess)
+            e = hipEventCreateWithFlags(&w.ev_up, hipEventDisableTiming);
         for (auto &ev : w.ev)
             if (e == hipSuccess)
                 e = hipEventCreate(&ev);
@@ -3357,6 +3381,10 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
         for (auto &ev : w.ev)
             if (ev)
                 (void)hipEventDestroy(ev);
+        if (w.ev_up)
+            (void)hipEventDestroy(w.ev_up);
+        if (w.upload)
+            (void)hipStreamDestroy(w.upload);
         if (w.stream)
             (void)hipStreamDestroy(w.stream);
     }
