@@ -1750,10 +1750,11 @@ __global__ void ung_addl_count_kernel(const uint32_t *__restrict__ gb, const uin
         atomicAdd(&cnt[1], my_entries);
 }
 
-// Additional edges, step 3: one wave per query row r (entry p = the last with row_off[p] <=
-// r, vector j = r - row_off[p] of C): an exact scan of X's range in the reference's
-// summation order and (dist, id) order, the first `per` results written to their final
-// place in the per-group edge lists (entries in LNG order, vectors, ranks).
+// Additional edges, step 3: one wave per LNG entry p = (C, X) with a target group of more
+// than ADDL_SMALL vectors, for each of its query rows j (vector j of C): an exact scan of
+// X's range in the reference's summation order and (dist, id) order, the first `per`
+// results written to their final place in the per-group edge lists (entries in LNG order,
+// vectors, ranks).
 struct AddlParams {
     const float *X;
     uint32_t d;
@@ -1764,66 +1765,122 @@ struct AddlParams {
     uint32_t *from, *to;
 };
 
+constexpr uint32_t ADDL_SMALL = 8; // target groups up to this size: one thread per entry
+
 __global__ __launch_bounds__(64) void ung_addl_scan_kernel(AddlParams A)
 {
     __shared__ float sd[64][33];
     __shared__ uint32_t si[64][33];
     const int lane = threadIdx.x;
-    const uint32_t R = A.row_off[A.E];
-    for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
-        uint32_t lo = 0, hi = A.E - 1; // the last entry p with row_off[p] <= r
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi + 1) >> 1;
-            if (A.row_off[mid] <= r)
-                lo = mid;
-            else
-                hi = mid - 1;
-        }
-        const uint32_t p = lo, j = r - A.row_off[p];
+    // one wave per LNG entry (grid-stride), its query rows one after the other; entries
+    // with no rows or a small target group are skipped (uniform: one wave per block)
+    for (uint32_t p = blockIdx.x; p < A.E; p += gridDim.x) {
+        const uint32_t m = A.row_off[p + 1] - A.row_off[p];
+        if (m == 0)
+            continue;
         const uint32_t c = A.eg[p], x = A.oi[p];
-        const uint32_t q = A.gb[c] + j;
         const uint32_t x0 = A.gb[x], x1 = A.gb[x + 1];
+        if (x1 - x0 <= ADDL_SMALL)
+            continue; // ung_addl_small_kernel's entry
         const uint32_t per = min(x1 - x0, A.per_max);
-        const float *qv = A.X + (size_t)q * A.d;
-        int32_t size = 0;
-        for (uint32_t g = x0 + (uint32_t)lane; g < x1; g += 64) {
-            const float dist = l2_ref_lane(qv, A.X + (size_t)g * A.d, A.d);
-            if (size == (int32_t)per && !cand_less(dist, g, sd[lane][size - 1], si[lane][size - 1]))
-                continue;
-            int32_t pos = size < (int32_t)per ? size : (int32_t)per - 1;
-            while (pos > 0 && cand_less(dist, g, sd[lane][pos - 1], si[lane][pos - 1])) {
-                sd[lane][pos] = sd[lane][pos - 1];
-                si[lane][pos] = si[lane][pos - 1];
-                --pos;
+        for (uint32_t j = 0; j < m; ++j) {
+            const uint32_t q = A.gb[c] + j;
+            const float *qv = A.X + (size_t)q * A.d;
+            int32_t size = 0;
+            for (uint32_t g = x0 + (uint32_t)lane; g < x1; g += 64) {
+                const float dist = l2_ref_lane(qv, A.X + (size_t)g * A.d, A.d);
+                if (size == (int32_t)per && !cand_less(dist, g, sd[lane][size - 1], si[lane][size - 1]))
+                    continue;
+                int32_t pos = size < (int32_t)per ? size : (int32_t)per - 1;
+                while (pos > 0 && cand_less(dist, g, sd[lane][pos - 1], si[lane][pos - 1])) {
+                    sd[lane][pos] = sd[lane][pos - 1];
+                    si[lane][pos] = si[lane][pos - 1];
+                    --pos;
+                }
+                sd[lane][pos] = dist;
+                si[lane][pos] = g;
+                if (size < (int32_t)per)
+                    ++size;
             }
-            sd[lane][pos] = dist;
-            si[lane][pos] = g;
-            if (size < (int32_t)per)
-                ++size;
-        }
-        int head = 0;
-        const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
-        for (uint32_t t = 0; t < per; ++t) {
-            const float hd = head < size ? sd[lane][head] : INFINITY;
-            const uint32_t hi2 = head < size ? si[lane][head] : NONE;
-            float bd = hd;
-            uint32_t bi = hi2;
-            for (int off = 32; off > 0; off >>= 1) {
-                const float od = __shfl_xor(bd, off);
-                const uint32_t oi2 = __shfl_xor(bi, off);
-                if (cand_less(od, oi2, bd, bi)) {
-                    bd = od;
-                    bi = oi2;
+            int head = 0;
+            const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
+            for (uint32_t t = 0; t < per; ++t) {
+                const float hd = head < size ? sd[lane][head] : INFINITY;
+                const uint32_t hi2 = head < size ? si[lane][head] : NONE;
+                float bd = hd;
+                uint32_t bi = hi2;
+                for (int off = 32; off > 0; off >>= 1) {
+                    const float od = __shfl_xor(bd, off);
+                    const uint32_t oi2 = __shfl_xor(bi, off);
+                    if (cand_less(od, oi2, bd, bi)) {
+                        bd = od;
+                        bi = oi2;
+                    }
+                }
+                if (bi != NONE && hi2 == bi)
+                    ++head;
+                if (lane == 0) {
+                    A.from[o + t] = q;
+                    A.to[o + t] = bi;
                 }
             }
-            if (bi != NONE && hi2 == bi)
-                ++head;
-            if (lane == 0) {
-                A.from[o + t] = q;
-                A.to[o + t] = bi;
+            __syncthreads();
+        }
+    }
+}
+
+// Additional edges, step 3 for target groups of at most ADDL_SMALL vectors: one thread per
+// LNG entry scans them for each of the entry's query rows (all candidates exact, ordered
+// by (dist, id) with an insertion network), writing the first `per` of each row; the wave
+// kernel above skips these rows.
+
+__global__ __launch_bounds__(256) void ung_addl_small_kernel(AddlParams A)
+{
+    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= A.E)
+        return;
+    const uint32_t m = A.row_off[p + 1] - A.row_off[p];
+    if (m == 0)
+        return;
+    const uint32_t c = A.eg[p], x = A.oi[p];
+    const uint32_t x0 = A.gb[x], nx = A.gb[x + 1] - x0;
+    if (nx > ADDL_SMALL)
+        return;
+    const uint32_t per = min(nx, A.per_max);
+    for (uint32_t j = 0; j < m; ++j) {
+        const uint32_t q = A.gb[c] + j;
+        const float *qv = A.X + (size_t)q * A.d;
+        float dv[ADDL_SMALL];
+        uint32_t iv[ADDL_SMALL];
+#pragma unroll
+        for (uint32_t t = 0; t < ADDL_SMALL; ++t) {
+            dv[t] = INFINITY;
+            iv[t] = NONE;
+            if (t < nx) {
+                dv[t] = l2_ref_lane(qv, A.X + (size_t)(x0 + t) * A.d, A.d);
+                iv[t] = x0 + t;
             }
         }
-        __syncthreads();
+        // insertion network under (dist, id): candidates arrive in id order
+#pragma unroll
+        for (int t = 1; t < (int)ADDL_SMALL; ++t)
+#pragma unroll
+            for (int u = t; u > 0; --u)
+                if (cand_less(dv[u], iv[u], dv[u - 1], iv[u - 1])) {
+                    const float td = dv[u];
+                    dv[u] = dv[u - 1];
+                    dv[u - 1] = td;
+                    const uint32_t ti = iv[u];
+                    iv[u] = iv[u - 1];
+                    iv[u - 1] = ti;
+                }
+        const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
+#pragma unroll
+        for (uint32_t t = 0; t < ADDL_SMALL; ++t)
+            if (t < per) {
+                A.from[o + t] = q;
+                A.to[o + t] = iv[t];
+            }
     }
 }
 
@@ -3136,7 +3193,9 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         A.per_max = num_cross / 2;
         A.from = ctx->a_from.p;
         A.to = ctx->a_to.p;
-        hipLaunchKernelGGL(ung_addl_scan_kernel, dim3(std::min<uint32_t>(R, 65536u)), dim3(64), 0, sm0, A);
+        hipLaunchKernelGGL(ung_addl_small_kernel, dim3((E + 255) / 256), dim3(256), 0, sm0, A);
+        HIPCHECK(hipGetLastError());
+        hipLaunchKernelGGL(ung_addl_scan_kernel, dim3(std::min<uint32_t>(E, 65536u)), dim3(64), 0, sm0, A);
         HIPCHECK(hipGetLastError());
     }
     hipLaunchKernelGGL(ung_addl_ptr_kernel, dim3((G + 2 + 255) / 256), dim3(256), 0, sm0, ctx->a_op.p, ctx->a_edges.p,
