@@ -682,8 +682,16 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     // thresholds may be shared between a query's queues only when one queue's LT
     // entries already cover the k results
     const bool share = P.k <= (uint32_t)LT;
-    // counting bound of the long queues (LT >= 16): 4*m4 >= Lp+1 (Lp = P.lp < 4*LT)
-    [[maybe_unused]] const uint32_t m4 = (P.lp + 4u) / 4u;
+    // counting bound: 4*m4 >= Lp+1 (Lp = P.lp < 4*LT)
+    const uint32_t m4 = (P.lp + 4u) / 4u;
+    // LT = 8: the counting bound replaces the other wave's share bound in sm.tau (it is
+    // the tighter one once the queues hold m4 entries); pm4o: this wave's value of the
+    // query after its latest tile
+    constexpr bool CNT8 = LT == 8;
+    [[maybe_unused]] float pm4o[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+        pm4o[nb] = INFINITY;
 
     // loader mapping: rows lr = (tid>>3) + RSTEP*m, columns c4 .. c4+3 of the chunk
     const int lr0 = tid >> 3;
@@ -901,11 +909,13 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 }
             }
             //
-            // Long queues (LT >= 16) also apply a counting bound, valid for any k: the
-            // query's four queues hold m4 entries each at or below the largest of their
+            // Queues of LT = 8 and LT >= 16 also apply a counting bound, valid for any k:
+            // the query's four queues hold m4 entries each at or below the largest of their
             // m4-th entries (4*m4 >= Lp+1 entries in all), so a candidate at or above that
             // value is not among the query's Lp+1 best.  The other wave's value is from the
-            // previous tile: entries only decrease, so it bounds the current one.
+            // previous tile: entries only decrease, so it bounds the current one.  (For
+            // k = 6, Lp = 10: the larger of the four queues' 3rd entries, near the query's
+            // 16th best, against about its 26th for the smallest of their 8th entries.)
             float tsh[NB], ncth[NB];
             [[maybe_unused]] float pm4[NB];
 #pragma unroll
@@ -916,9 +926,12 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 float t = fminf(own, tfin[nb]);
                 if (share) {
                     t = fminf(t, partner);
-                    if (tile > 0)
+                    if (!CNT8 && tile > 0)
                         t = fminf(t, sm.tau[(tile - 1) & 1][wm ^ 1][col]);
                 }
+                if constexpr (CNT8)
+                    if (tile > 0)
+                        t = fminf(t, fmaxf(pm4o[nb], sm.tau[(tile - 1) & 1][wm ^ 1][col]));
                 if constexpr (LT >= 16) {
                     float o4 = INFINITY;
 #pragma unroll
@@ -1119,9 +1132,19 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 // publish this wave's threshold of the query for the other wave
                 const float t = fminf(tsh[nb], ld[nb][LT - 1]);
                 tfin[nb] = t;
-                const float pair_t = fminf(t, __shfl_xor(t, 32));
-                if (share && h == 0)
-                    sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
+                if constexpr (CNT8) {
+                    float o4 = INFINITY;
+#pragma unroll
+                    for (int j = 0; j < LT; ++j)
+                        o4 = (uint32_t)j + 1u == m4 ? ld[nb][j] : o4;
+                    pm4o[nb] = fmaxf(o4, __shfl_xor(o4, 32));
+                    if (h == 0)
+                        sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pm4o[nb];
+                } else {
+                    const float pair_t = fminf(t, __shfl_xor(t, 32));
+                    if (share && h == 0)
+                        sm.tau[tile & 1][wm][wn * QW + nb * 32 + r] = pair_t;
+                }
                 if constexpr (LT >= 16)
                     if (h == 0)
                         tau4.v[tile & 1][wm][wn * QW + nb * 32 + r] = pm4[nb];
