@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the UNG cross-edge + mid-group kNN build stage on one MI355X.
 
-Workload ("cfg2"): 1M x 128 fp32 vectors from a
+Workload "cfg2" (the headline configuration): 1M x 128 fp32 vectors from a
 1000-centroid Gaussian mixture, 40 labels (1-4 per vector, Zipf 1.2), k=6 cross
 edges per vector and exact K=32 intra-group kNN for every mid-size group
 (128 <= n <= 4096).  Synthetic, seeded data (no network).
@@ -135,7 +135,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (one-GPU boxes); "
-                                   "multi-GPU sharding is design-only, see DESIGN.md", "n_gpus": args.gpus}))
+                                   "multi-GPU sharding is not built", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import filtervectorcode_refactor_amd as F
