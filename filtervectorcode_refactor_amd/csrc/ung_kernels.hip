@@ -238,7 +238,9 @@ __device__ __forceinline__ float l2_ref_lane(const float *__restrict__ a,
 
 // Sorted insert of (nd, ni) into an ascending register queue (ties keep the older
 // entry first; nd = +inf changes nothing).  Runs from the tail so every entry is
-// updated in place from the old values of itself and its predecessor.
+// updated in place from the old values of itself and its predecessor.  The new
+// distance at j is the median of (old j-1, nd, old j) -- one v_med3_f32, which returns
+// one of its inputs exactly; the id follows the same choice by the two comparisons.
 template <int LT>
 __device__ __forceinline__ void list_insert(float (&ld)[LT], uint32_t (&li)[LT], float nd,
                                             uint32_t ni)
@@ -247,7 +249,7 @@ __device__ __forceinline__ void list_insert(float (&ld)[LT], uint32_t (&li)[LT],
 #pragma unroll
     for (int j = LT - 1; j > 0; --j) {
         const bool c_lo = nd < ld[j - 1];
-        ld[j] = c_hi ? (c_lo ? ld[j - 1] : nd) : ld[j];
+        ld[j] = __builtin_amdgcn_fmed3f(ld[j - 1], nd, ld[j]);
         li[j] = c_hi ? (c_lo ? li[j - 1] : ni) : li[j];
         c_hi = c_lo;
     }
@@ -995,7 +997,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     const float av = staged(j);
                     const uint32_t rid = sm.rowid[slot][tile_row(wm, h, j)];
                     float dd = __builtin_fmaf(-2.0f, av, qnv[nb]);
-                    dd = (act && dd < fminf(ld[nb][LT - 1], tsh[nb])) ? dd : INFINITY;
+                    dd = (act && dd < ld[nb][LT - 1] && dd < tsh[nb]) ? dd : INFINITY;
                     list_insert<LT>(ld[nb], li[nb], dd, rid);
                 }
             };
@@ -1047,10 +1049,10 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                         const uint32_t nr = round_count(pend[nb]);
                         bool merged = false;
                         if constexpr (LT == 32) {
-                            // an early tile of a long queue: more than ~12 rounds (about 175
+                            // an early tile of a long queue: more than ~14 rounds (about 142
                             // instructions each) cost more than merging the tile's 32 entries
                             // with a sorting network
-                            if (nr > 12u) {
+                            if (nr > 14u) {
                                 float dv[32];
                                 uint32_t iv[32];
 #pragma unroll

@@ -115,7 +115,7 @@ def _two_level_problem(rng, sizes_children, sizes_targets, dim, dup=False):
 
 
 @pytest.mark.parametrize("dim,k,seed", [(128, 6, 1), (37, 6, 2), (12, 1, 3), (64, 64, 4), (128, 20, 5),
-                                        (768, 6, 6), (5, 6, 7)])
+                                        (768, 6, 6), (5, 6, 7), (128, 12, 8), (40, 16, 9), (128, 8, 10)])
 def test_cross_edge_cases(ctx, oracle, dim, k, seed):
     rng = np.random.default_rng(seed)
     _say(f"cross edge case dim={dim} k={k}")
@@ -143,7 +143,8 @@ def test_cross_multi_split(ctx, oracle):
 
 
 @pytest.mark.parametrize("n,list_k,dim", [(2, 32, 128), (3, 1, 16), (129, 32, 128), (200, 64, 40), (700, 32, 384),
-                                          (20000, 8, 64), (300, 6, 128), (1000, 8, 128)])
+                                          (20000, 8, 64), (300, 6, 128), (1000, 8, 128), (500, 16, 128),
+                                          (600, 12, 72)])
 def test_intra_edge_cases(ctx, oracle, n, list_k, dim):
     rng = np.random.default_rng(n)
     _say(f"intra edge case n={n} k={list_k} dim={dim}")
