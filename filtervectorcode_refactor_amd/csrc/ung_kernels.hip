@@ -462,26 +462,19 @@ __device__ __forceinline__ uint32_t lane_index_of(int o)
     return (o >= 0 && o < 64 && (o & 4) == 0) ? (((uint32_t)o >> 1) & 28u) | ((uint32_t)o & 3u) : 32u;
 }
 
-// Compare-exchange of entries a < b of a register queue (ascending by distance).  The
-// swap mask is the sign of d[b] - d[a] (all ones iff d[b] < d[a] for the non-negative,
-// possibly infinite distances here; inf - inf gives a NaN that swaps two +inf entries
-// at most), applied with bit selects, so no lane-mask registers stay live across the
-// interleaved exchanges of a network.
-__device__ __forceinline__ uint32_t bitsel(uint32_t m, uint32_t a, uint32_t b)
-{
-    return (a & m) | (b & ~m);
-}
+// Compare-exchange of entries a < b of a register queue (ascending by distance): one
+// comparison and four selects (equal entries, two +inf included, stay in place).
 
 template <int N>
 __device__ __forceinline__ void cas(float (&d)[N], uint32_t (&id)[N], int a, int b)
 {
-    const uint32_t da = __float_as_uint(d[a]), db = __float_as_uint(d[b]);
-    const uint32_t m = (uint32_t)((int32_t)__float_as_uint(d[b] - d[a]) >> 31);
-    d[a] = __uint_as_float(bitsel(m, db, da));
-    d[b] = __uint_as_float(bitsel(m, da, db));
+    const float da = d[a], db = d[b];
+    const bool sw = db < da;
+    d[a] = sw ? db : da;
+    d[b] = sw ? da : db;
     const uint32_t ia = id[a], ib = id[b];
-    id[a] = bitsel(m, ib, ia);
-    id[b] = bitsel(m, ia, ib);
+    id[a] = sw ? ib : ia;
+    id[b] = sw ? ia : ib;
 }
 
 // Ascending bitonic sort of the 8 entries at base..base+7 (24 compare-exchanges).
@@ -512,9 +505,9 @@ __device__ __forceinline__ void merge8_keep(float (&d)[N], uint32_t (&id)[N], in
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int l = b + 7 - i;
-        const uint32_t m = (uint32_t)((int32_t)__float_as_uint(d[l] - d[a + i]) >> 31);
-        d[a + i] = __uint_as_float(bitsel(m, __float_as_uint(d[l]), __float_as_uint(d[a + i])));
-        id[a + i] = bitsel(m, id[l], id[a + i]);
+        const bool t = d[l] < d[a + i];
+        d[a + i] = t ? d[l] : d[a + i];
+        id[a + i] = t ? id[l] : id[a + i];
     }
 #pragma unroll
     for (int j = 4; j > 0; j >>= 1)
@@ -590,9 +583,9 @@ __device__ __forceinline__ void merge_into_queue32(float (&d)[32], uint32_t (&id
     sort32(d, id);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        const uint32_t m = (uint32_t)((int32_t)__float_as_uint(d[31 - i] - ld[i]) >> 31);
-        ld[i] = __uint_as_float(bitsel(m, __float_as_uint(d[31 - i]), __float_as_uint(ld[i])));
-        li[i] = bitsel(m, id[31 - i], li[i]);
+        const bool t = d[31 - i] < ld[i];
+        ld[i] = t ? d[31 - i] : ld[i];
+        li[i] = t ? id[31 - i] : li[i];
     }
 #pragma unroll
     for (int j = 16; j > 0; j >>= 1)
@@ -1049,10 +1042,10 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                         const uint32_t nr = round_count(pend[nb]);
                         bool merged = false;
                         if constexpr (LT == 32) {
-                            // an early tile of a long queue: more than ~14 rounds (about 142
+                            // an early tile of a long queue: more than ~13 rounds (about 142
                             // instructions each) cost more than merging the tile's 32 entries
-                            // with a sorting network
-                            if (nr > 14u) {
+                            // with a sorting network (about 1,900)
+                            if (nr > 13u) {
                                 float dv[32];
                                 uint32_t iv[32];
 #pragma unroll
