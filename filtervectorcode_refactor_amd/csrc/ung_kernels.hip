@@ -275,6 +275,20 @@ __device__ __forceinline__ float lower_bound_exact(float A, float qn, double eps
     return __double2float_rd(b);
 }
 
+// Upper bound on the exact (reference-rounded) distance of a candidate whose
+// expansion-form MFMA distance is A (the same two error terms, the other way; the
+// exact distance is >= 0).  Rounded toward +inf.
+__device__ __forceinline__ float upper_bound_exact(float A, float qn, double eps_coef, double shrink, double rmax)
+{
+    if (!(A < INFINITY))
+        return INFINITY;
+    const double qnorm = sqrt((double)fmaxf(qn, 0.0f) * (1.0 + 1e-6));
+    const double r = qnorm + rmax;
+    const double ea = eps_coef * r * r;
+    const double b = fmax((double)A + ea, 0.0) * (1.0 + shrink) + 1e-30;
+    return __double2float_ru(b);
+}
+
 // (dist, id) argmin across the wave; every lane ends with the minimum.
 __device__ __forceinline__ void wave_argmin(float &d, uint32_t &i)
 {
@@ -1258,6 +1272,7 @@ struct MergeParams {
 __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams M)
 {
     __shared__ uint32_t mrank[MERGE_ROWS][128]; // a wave's candidates in rank order
+    __shared__ float mrankd[MERGE_ROWS][128];   // and their approximate distances
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const MergeItem mi = M.mitems[blockIdx.x];
     if ((uint32_t)w >= mi.q_cnt)
@@ -1268,15 +1283,19 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
     const uint32_t S = jb.n_split, Lp = M.lp, k = M.k;
 
     // slot h of lane t holds the (64h + t)-th smallest approximate candidate (Lp <= 128)
+    // and its approximate distance
     uint32_t ci[2] = {NONE, NONE};
+    float ca[2] = {INFINITY, INFINITY};
     float B; // approximate-space bound of every candidate left out
     if (S == 1) {
         // one split: its partial row is already the approximate top-Lp
         const size_t prow = (size_t)jb.part_base + ql;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-            if ((uint32_t)(64 * h + lane) < Lp)
+            if ((uint32_t)(64 * h + lane) < Lp) {
                 ci[h] = M.part_ids[prow * Lp + 64 * h + lane];
+                ca[h] = M.part_dist[prow * Lp + 64 * h + lane];
+            }
         B = M.part_bound[prow];
     } else if (S * Lp <= 128u) {
         // all S*Lp entries in the wave (two per lane): each entry's rank under (dist, id,
@@ -1327,16 +1346,20 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const bool in = 64u * (uint32_t)h + (uint32_t)lane < n;
-            if (in && rk[h] < Lp)
+            if (in && rk[h] < Lp) {
                 mrank[w][rk[h]] = eid[h];
+                mrankd[w][rk[h]] = ed[h];
+            }
             if (in && rk[h] == Lp)
                 a_next = ed[h];
         }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-            if (64u * (uint32_t)h + (uint32_t)lane < Lp)
+            if (64u * (uint32_t)h + (uint32_t)lane < Lp) {
                 ci[h] = mrank[w][64 * h + lane];
+                ca[h] = mrankd[w][64 * h + lane];
+            }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1)
             a_next = fminf(a_next, __shfl_xor(a_next, off));
@@ -1368,10 +1391,13 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
                 break;
             }
             if ((uint32_t)lane == (t & 63u)) {
-                if (t < 64)
+                if (t < 64) {
                     ci[0] = bi;
-                else
+                    ca[0] = bd;
+                } else {
                     ci[1] = bi;
+                    ca[1] = bd;
+                }
             }
             if (hi == bi) {
                 ++pos;
@@ -1387,13 +1413,40 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
         B = fminf(bmin, a_next);
     }
 
+    // Only candidates that can be among the k best are re-scored: the k best by
+    // approximate distance all have exact distances <= U = upper_bound_exact(a_{k-1}), so
+    // the k-th exact distance T <= U, and a candidate whose lower bound exceeds U has an
+    // exact distance > T (it is neither a result nor needed by the certificate).  The
+    // candidates are in ascending approximate order, so the re-scored ones are a prefix.
+    const float xq = M.xn[q];
+    uint32_t m_need = Lp;
+    if (k <= Lp) {
+        const int src = (int)((k - 1u) & 63u);
+        const float ak = k - 1u < 64u ? __shfl(ca[0], src) : __shfl(ca[1], src);
+        const float U = upper_bound_exact(ak, xq, M.eps_coef, M.shrink, M.rmax);
+        if (U < INFINITY) {
+            uint32_t cnt_need = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const bool in = (uint32_t)(64 * h + lane) < Lp;
+                const bool need = in && !(lower_bound_exact(ca[h], xq, M.eps_coef, M.shrink, M.rmax) > U);
+                cnt_need += (uint32_t)__popcll(__ballot(need));
+            }
+            m_need = cnt_need;
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if ((uint32_t)(64 * h + lane) >= m_need)
+            ci[h] = NONE; // left out (exact distance > T): not a result
+
     // exact re-score: 8 lanes per candidate (one per accumulator of the reference's
     // summation), 8 candidates per pass; candidate t's value goes to lane t % 64, slot t / 64
     const float *qv = M.X + (size_t)q * M.d;
     float ex[2] = {INFINITY, INFINITY};
     {
         const int g = lane >> 3, sub = lane & 7;
-        const uint32_t npass = (Lp + 7u) / 8u;
+        const uint32_t npass = (m_need + 7u) / 8u;
         for (uint32_t p = 0; p < npass; ++p) {
             const uint32_t t = 8u * p + (uint32_t)g;
             const int src = (int)(t & 63u);
@@ -1410,9 +1463,10 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
             }
         }
     }
-    // rank under (exact, id, position)
+    // rank under (exact, id, position); a left-out candidate (exact distance > T) ranks
+    // after every re-scored one and takes no place in the row
     uint32_t rank[2] = {0u, 0u};
-    for (uint32_t f = 0; f < Lp; ++f) {
+    for (uint32_t f = 0; f < m_need; ++f) {
         const int src = (int)(f & 63u);
         const float df = f < 64 ? __shfl(ex[0], src) : __shfl(ex[1], src);
         const uint32_t idf = f < 64 ? __shfl(ci[0], src) : __shfl(ci[1], src);
@@ -1427,7 +1481,7 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
     uint32_t cnt = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        mine[h] = (uint32_t)(64 * h + lane) < Lp;
+        mine[h] = (uint32_t)(64 * h + lane) < m_need;
         real[h] = mine[h] && ci[h] != NONE;
         T = (mine[h] && rank[h] == k - 1) ? ex[h] : T;
         cnt += (uint32_t)__popcll(__ballot(real[h] && rank[h] < k));
@@ -1435,7 +1489,7 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
         T = fminf(T, __shfl_xor(T, off));
-    const float Bx = lower_bound_exact(B, M.xn[q], M.eps_coef, M.shrink, M.rmax);
+    const float Bx = lower_bound_exact(B, xq, M.eps_coef, M.shrink, M.rmax);
     const bool certified = (cnt < k) ? !(B < INFINITY) : (T < Bx);
     if (!certified) {
         if (lane == 0) {
