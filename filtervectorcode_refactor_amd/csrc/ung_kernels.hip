@@ -1120,16 +1120,28 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     } else {
                         // element j of the list through a select tree over its 32
                         // accumulator values (bit 4 of j: the half, bits 3..0: the entry)
+                        // (each level's bit of j sign-extended to a lane mask by one
+                        // bit-field extract; each select one bit-select instruction)
                         auto pick = [&](uint32_t j) -> float {
+                            auto sel = [](uint32_t m, float a, float b) {
+                                return __uint_as_float((__float_as_uint(a) & m) | (__float_as_uint(b) & ~m));
+                            };
+                            // (the empty asm keeps the compiler from turning the masks
+                            // back into compares and lane-mask selects)
                             float v[16];
+                            uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)j, 4, 1);
+                            asm("" : "+v"(m));
 #pragma unroll
                             for (int i = 0; i < 16; ++i)
-                                v[i] = (j & 16u) ? acc[1][nb][i] : acc[0][nb][i];
+                                v[i] = sel(m, acc[1][nb][i], acc[0][nb][i]);
 #pragma unroll
-                            for (int w = 8; w >= 1; w >>= 1)
+                            for (int w = 8, b = 3; w >= 1; w >>= 1, --b) {
+                                m = (uint32_t)__builtin_amdgcn_sbfe((int)j, b, 1);
+                                asm("" : "+v"(m));
 #pragma unroll
                                 for (int i = 0; i < w; ++i)
-                                    v[i] = (j & (uint32_t)w) ? v[i + w] : v[i];
+                                    v[i] = sel(m, v[i + w], v[i]);
+                            }
                             return v[0];
                         };
                         rounds(nb, pend[nb], round_count(pend[nb]), pick);
