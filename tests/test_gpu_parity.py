@@ -157,6 +157,33 @@ def test_intra_edge_cases(ctx, oracle, n, list_k, dim):
     _assert_rows_equal(ids, dist, None, oi, od, None, f"intra n={n}")
 
 
+@pytest.mark.parametrize("dim,k", [(128, 6), (24, 16)])
+def test_cross_integer_ties(ctx, oracle, dim, k):
+    """Coordinates in {0, 1, 2}: many candidates share the k-th distance exactly, so the
+    (dist, id) order decides and no candidate at the k-th distance may be left out of
+    the exact re-score."""
+    rng = np.random.default_rng(dim + k)
+    _say(f"cross integer ties dim={dim} k={k}")
+    _, gb, op, oi = _two_level_problem(rng, [40, 130, 7], [300, 2, 129, 50], dim)
+    X = rng.integers(0, 3, size=(int(gb[-1]), dim)).astype(np.float32)
+    ctx.prepare_vectors(X)
+    ids, dist, size, stats = ctx.cross_topk(gb, op, oi, k)
+    ip, ii = F.in_neighbors(op, oi)
+    o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, k)
+    _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, f"integer ties dim={dim} k={k}")
+
+
+@pytest.mark.parametrize("n,list_k,dim", [(300, 32, 128), (150, 8, 16)])
+def test_intra_integer_ties(ctx, oracle, n, list_k, dim):
+    rng = np.random.default_rng(n + dim)
+    _say(f"intra integer ties n={n} k={list_k} dim={dim}")
+    X = rng.integers(0, 3, size=(n + 10, dim)).astype(np.float32)
+    ctx.prepare_vectors(X)
+    ids, dist, stats = ctx.group_knn([5], [n], list_k)
+    oi, od = oracle.intra_exact(X, 5, n, list_k)
+    _assert_rows_equal(ids, dist, None, oi, od, None, f"intra integer ties n={n}")
+
+
 def test_errors(ctx):
     X = np.zeros((10, 8), np.float32)
     ctx.prepare_vectors(X)
