@@ -2407,6 +2407,9 @@ struct ung_hip_ctx {
     Workspace ws[2];
     // a group call in flight on ws[1] (ung_hip_cross_intra_begin .. ung_hip_intra_end)
     bool intra_pending = false;
+    // work lists of the calls on ws[0] (one at a time), kept between calls so their
+    // storage is reused instead of allocated and first touched again every call
+    Plan plan0;
     Plan intra_plan;
     uint32_t intra_list_k = 0;
     ung_hip_stats intra_stats{};
@@ -2456,6 +2459,21 @@ uint32_t split_size(uint64_t u)
     uint64_t s = (u + MAX_SPLITS - 1) / MAX_SPLITS;
     s = (s + BC - 1) / BC * BC;
     return (uint32_t)std::max<uint64_t>(SPLIT_V, s);
+}
+
+// Empties a plan, keeping the capacity of its lists.
+void plan_reset(Plan &pl)
+{
+    pl.jobs.clear();
+    pl.items.clear();
+    pl.pitems.clear();
+    pl.seg_start.clear();
+    pl.seg_vend.clear();
+    pl.n_mitems = 0;
+    pl.part_rows = 0;
+    pl.pairs = 0;
+    pl.padded = 0;
+    pl.rows = 0;
 }
 
 void add_items_for_job(Plan &pl, uint32_t job_index)
@@ -2930,7 +2948,8 @@ int cross_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, cons
     if ((rc = set_device(ctx)))
         return rc;
     const auto t0 = clk::now();
-    Plan pl;
+    Plan &pl = ctx->plan0;
+    plan_reset(pl);
     if ((rc = build_cross_plan(ctx, G, group_begin, out_ptr, out_idx, pl)))
         return rc;
     if (st)
@@ -2961,7 +2980,8 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     if ((rc = set_device(ctx)))
         return rc;
     const auto t0 = clk::now();
-    Plan pl;
+    Plan &pl = ctx->plan0;
+    plan_reset(pl);
     if ((rc = build_cross_plan(ctx, G, group_begin, out_ptr, out_idx, pl)))
         return rc;
     if (st)
@@ -2971,7 +2991,7 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     // the group call is planned while the cross kernels run
     ctx->intra_stats = ung_hip_stats{};
     ctx->intra_t0 = clk::now();
-    ctx->intra_plan = Plan{};
+    plan_reset(ctx->intra_plan);
     if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, ctx->intra_plan)))
         return rc;
     ctx->intra_stats.plan_ms += ms_since(ctx->intra_t0);
@@ -3130,7 +3150,8 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
     if ((rc = set_device(ctx)))
         return rc;
     const auto t0 = clk::now();
-    Plan pl;
+    Plan &pl = ctx->plan0;
+    plan_reset(pl);
     if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, pl)))
         return rc;
     if (st)
