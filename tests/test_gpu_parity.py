@@ -184,6 +184,34 @@ def test_intra_integer_ties(ctx, oracle, n, list_k, dim):
     _assert_rows_equal(ids, dist, None, oi, od, None, f"intra integer ties n={n}")
 
 
+def test_cross_many_lists(ctx, oracle):
+    """An LNG with more than 2^18 out-list entries, groups without points among the
+    targets, and an out-of-range entry rejected."""
+    rng = np.random.default_rng(77)
+    G = 4000
+    sizes = rng.integers(0, 4, size=G)  # some groups without points
+    gb = np.zeros(G + 2, np.uint32)
+    gb[2:] = np.cumsum(sizes)
+    rows = [np.sort(rng.choice(np.setdiff1d(np.arange(1, G + 1), [c]), size=70, replace=False))
+            for c in range(1, G + 1)]
+    op = np.zeros(G + 2, np.uint32)
+    op[2:] = np.cumsum([len(r) for r in rows])
+    oi = np.concatenate(rows).astype(np.uint32)
+    assert len(oi) >= (1 << 18)
+    X = rng.standard_normal((int(gb[-1]), 16)).astype(np.float32)
+    _say(f"cross many lists G={G} entries={len(oi)}")
+    ctx.prepare_vectors(X)
+    ids, dist, size, stats = ctx.cross_topk(gb, op, oi, 6)
+    ip, ii = F.in_neighbors(op, oi)
+    o_ids, o_d, o_s = oracle.cross_exact(X, gb, ip, ii, 6)
+    _assert_rows_equal(ids, dist, size, o_ids, o_d, o_s, "many lists")
+    with pytest.raises(F.UngHipError):
+        bad = oi.copy()
+        c = int(np.nonzero(sizes)[0][-1]) + 1  # the last group with points reads its list
+        bad[int(op[c]) + 3] = G + 1
+        ctx.cross_topk(gb, op, bad, 6)
+
+
 def test_errors(ctx):
     X = np.zeros((10, 8), np.float32)
     ctx.prepare_vectors(X)
