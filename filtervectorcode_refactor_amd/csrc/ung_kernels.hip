@@ -878,10 +878,14 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                         acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[mb], bh[nb], acc[mb][nb], 0, 0, 0);
             }
         };
+        // the MFMA block at raised wave priority: the SIMD's other wave (in its epilogue's
+        // VALU work) yields issue slots to it, which keeps the matrix core fed
+        __builtin_amdgcn_s_setprio(1);
         if (kc == 0)
             mfma_chunk(std::true_type{});
         else
             mfma_chunk(std::false_type{});
+        __builtin_amdgcn_s_setprio(0);
         // next tile's row ids: issued after this step's MFMAs, visible after the next
         // step's barrier, consumed by the prefetch of the tile's first chunk (at step
         // nk-1 >= 1); the |x|^2 values are stored at the top of step 1
