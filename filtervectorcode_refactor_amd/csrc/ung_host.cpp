@@ -341,12 +341,96 @@ extern "C" int ung_group_label_sets(uint64_t N, const uint32_t *lab_ptr, const u
 }
 
 // ---------------------------------------------------------------------------
+// Row order of the label navigating graph.
+//
+// The reference lists out(C) as the minimal supersets in label-set-size order, and
+// within one size in the order its trie walk discovers them
+// (get_min_super_sets_optimized_bucket, src/uni_nav_graph_label_graph.cpp:103-206,
+// over TrieIndex::get_super_set_entrances, src/trie.cpp:78-143).  The walk is a
+// breadth-first search that starts from the trie nodes carrying C's largest label L
+// whose path holds all of C (in the order those nodes were created) and visits each
+// node's children in the iteration order of its std::unordered_map.  Breadth-first
+// order over that forest is lexicographic order of
+//   (levels below the start node, creation index of the start node,
+//    child rank at each level from the start node down),
+// so the rows are sorted by (set size, that key).  The trie is rebuilt here from
+// the group label sets in group id order (first appearance, which creates the nodes
+// in the reference's order) with an std::unordered_map per node filled by the same
+// sequence of insertions, which reproduces its iteration order.  An empty C starts
+// from the root's children (the root's own rank path).
+// ---------------------------------------------------------------------------
+namespace {
+
+struct LabelTrie {
+    std::vector<uint32_t> parent, label, depth, rank, created; // per node (0 = root)
+    std::vector<uint32_t> group_node;                          // per group id
+
+    LabelTrie(uint32_t G, const uint32_t *set_ptr, const uint32_t *set_idx)
+    {
+        std::vector<std::unordered_map<uint32_t, uint32_t>> kids(1);
+        std::unordered_map<uint32_t, uint32_t> made_with_label;
+        parent.push_back(0);
+        label.push_back(0);
+        depth.push_back(0);
+        created.push_back(0);
+        group_node.assign((size_t)G + 1, 0);
+        for (uint32_t g = 1; g <= G; ++g) {
+            uint32_t cur = 0;
+            for (uint32_t i = set_ptr[g]; i < set_ptr[g + 1]; ++i) {
+                const uint32_t l = set_idx[i];
+                auto it = kids[cur].find(l);
+                if (it == kids[cur].end()) {
+                    const uint32_t nd = (uint32_t)parent.size();
+                    parent.push_back(cur);
+                    label.push_back(l);
+                    depth.push_back(depth[cur] + 1);
+                    created.push_back(made_with_label[l]++);
+                    kids[cur].emplace(l, nd);
+                    kids.emplace_back();
+                    cur = nd;
+                } else {
+                    cur = it->second;
+                }
+            }
+            group_node[g] = cur;
+        }
+        rank.assign(parent.size(), 0);
+        for (auto &m : kids) {
+            uint32_t r = 0;
+            for (const auto &kv : m)
+                rank[kv.second] = r++;
+        }
+    }
+
+    // key of group x in the row of a group whose largest label is L (has_L false: empty
+    // label set): [depth(x), levels below the start node, start node's creation index,
+    // child ranks from the start node down]
+    void key(uint32_t x, bool has_L, uint32_t L, std::vector<uint32_t> &out) const
+    {
+        out.clear();
+        uint32_t nd = group_node[x];
+        const uint32_t dx = depth[nd];
+        std::vector<uint32_t> &path = out; // ranks bottom-up, reversed below
+        while (nd != 0 && !(has_L && label[nd] == L)) {
+            path.push_back(rank[nd]);
+            nd = parent[nd];
+        }
+        const uint32_t levels = (uint32_t)path.size();
+        const uint32_t start = has_L ? created[nd] : 0;
+        std::reverse(path.begin(), path.end());
+        path.insert(path.begin(), {dx, levels, start});
+    }
+};
+
+} // namespace
+
+// ---------------------------------------------------------------------------
 // Label navigating graph: minimum proper supersets.
 // Candidates of C are found by intersecting label posting lists (every superset
 // of C contains each of C's labels); they are scanned by increasing set size and
 // a candidate is kept unless it contains an already-kept one, which yields
 // exactly the minimal elements (a non-minimal superset contains a minimal one of
-// smaller size).
+// smaller size).  Each row is then put in the reference's order (LabelTrie).
 // ---------------------------------------------------------------------------
 extern "C" int ung_lng_build(uint32_t G, const uint32_t *set_ptr, const uint32_t *set_idx,
                              uint32_t *out_ptr, uint32_t *out_idx, uint64_t out_cap,
@@ -388,9 +472,11 @@ extern "C" int ung_lng_build(uint32_t G, const uint32_t *set_ptr, const uint32_t
     for (uint32_t g = 1; g <= G; ++g)
         all_groups[g - 1] = g;
 
+    const LabelTrie trie(G, set_ptr, set_idx);
     std::vector<std::vector<uint32_t>> rows(G + 1);
     parallel_for((int64_t)G, nthreads, 64, [&](int64_t b, int64_t e) {
         std::vector<uint32_t> cand, kept;
+        std::vector<std::pair<std::vector<uint32_t>, uint32_t>> keyed;
         for (int64_t gi = b; gi < e; ++gi) {
             const uint32_t c = (uint32_t)gi + 1;
             const uint32_t lc = len_of(c);
@@ -417,7 +503,18 @@ extern "C" int ung_lng_build(uint32_t G, const uint32_t *set_ptr, const uint32_t
                 if (minimal)
                     kept.push_back(x);
             }
-            std::sort(kept.begin(), kept.end());
+            if (kept.size() > 1) {
+                const bool has_L = lc > 0;
+                const uint32_t L = has_L ? set_idx[set_ptr[c + 1] - 1] : 0;
+                keyed.resize(kept.size());
+                for (size_t i = 0; i < kept.size(); ++i) {
+                    trie.key(kept[i], has_L, L, keyed[i].first);
+                    keyed[i].second = kept[i];
+                }
+                std::sort(keyed.begin(), keyed.end());
+                for (size_t i = 0; i < kept.size(); ++i)
+                    kept[i] = keyed[i].second;
+            }
             rows[c] = kept;
         }
     });

@@ -264,7 +264,29 @@ class RefOracle:
         L.ungref_assemble_graph.argtypes = _ASM_ARGS
         L.ungref_graph_save.restype = None
         L.ungref_graph_save.argtypes = [C.c_char_p, C.c_uint64, C.POINTER(C.c_uint64), _u32p]
+        L.ungref_trie_lng.restype = C.c_int64
+        L.ungref_trie_lng.argtypes = [C.c_uint64, _u32p, _u32p, _u32p, C.POINTER(C.c_uint32), _u32p, _u32p,
+                                      C.c_int64]
         self.lib = L
+
+    def trie_lng(self, lab_ptr, lab_idx):
+        """Groups and LNG with the reference's own TrieIndex (ungref_trie_lng):
+        (G, point_group[N], out_ptr[G+2], out_idx) -- rows in the reference's order."""
+        lab_ptr = _u32(lab_ptr)
+        lab_idx = _u32(lab_idx) if len(lab_idx) else np.zeros(1, np.uint32)
+        N = lab_ptr.shape[0] - 1
+        pg = np.zeros(max(N, 1), np.uint32)
+        G = C.c_uint32(0)
+        out_ptr = np.zeros(N + 2, np.uint32)
+        cap = max(4 * N, 16)
+        while True:
+            out_idx = np.zeros(cap, np.uint32)
+            n = self.lib.ungref_trie_lng(N, lab_ptr, lab_idx, pg, C.byref(G), out_ptr, out_idx, cap)
+            if n <= cap:
+                break
+            cap = int(n)
+        g = G.value
+        return g, pg[:N].copy(), out_ptr[: g + 2].copy(), out_idx[:n].copy()
 
     def l2(self, a, b) -> float:
         a, b = _f32(a), _f32(b)

@@ -1,7 +1,8 @@
 // ref_driver.cpp -- thin C entry points around the reference's OWN compiled
-// FloatL2DistanceHandler (UNG/codes/src/distance.cpp) and SearchQueue
-// (UNG/codes/src/search_queue.cpp), built into oracle/_ref/libungref.so by
-// oracle/Makefile directly from /root/reference (nothing copied into this repo).
+// FloatL2DistanceHandler (UNG/codes/src/distance.cpp), SearchQueue
+// (UNG/codes/src/search_queue.cpp) and TrieIndex (UNG/codes/src/trie.cpp), built into
+// oracle/_ref/libungref.so by oracle/Makefile directly from /root/reference (nothing
+// copied into this repo).
 //
 // TEST INFRASTRUCTURE ONLY: used to pin the plain-C oracle (oracle/ung_oracle.c),
 // to write tests/golden fixtures, and as the "reference" CPU baseline in bench.py.
@@ -15,6 +16,9 @@
 //                          (src/uni_nav_graph_special_blocks.cpp:70-111)
 //   ungref_additional_edges -> build_cross_edges_generate_additional, exact branch
 //                          (src/uni_nav_graph_cross_edges.cpp:442-596)
+//   ungref_trie_lng     -> build_trie_and_divide_groups + LNG phase 1 with
+//                          get_min_super_sets_optimized_bucket around the compiled
+//                          TrieIndex (src/uni_nav_graph_label_graph.cpp:21-43,103-206,851-890)
 //   ungref_assemble_graph / ungref_graph_save -> the reference's own Graph/NeighborList
 //                          (include/graph.h) filled as add_offset_for_uni_nav_graph,
 //                          merge_cross_edges_to_graph and merge_additional_edges_to_graph
@@ -24,6 +28,7 @@
 #include <cmath>
 #include <cstdint>
 #include <limits>
+#include <memory>
 #include <utility>
 #include <vector>
 #include <omp.h>
@@ -31,6 +36,7 @@
 #include "distance.h"
 #include "graph.h"
 #include "search_queue.h"
+#include "trie.h"
 
 using ANNS::FloatL2DistanceHandler;
 using ANNS::SearchQueue;
@@ -276,6 +282,101 @@ int64_t ungref_assemble_graph(uint64_t N, uint32_t G, const uint32_t *group_begi
         row_ptr[i + 1] = (uint64_t)n;
     }
     return n <= cap ? n : -1;
+}
+
+// Group division and label navigating graph with the reference's OWN TrieIndex
+// (src/trie.cpp, compiled into this library):
+//   * build_trie_and_divide_groups (src/uni_nav_graph_label_graph.cpp:21-43): every
+//     vector's label set inserted in vector order; point_group[i] = its group id;
+//   * phase 1 of build_label_nav_graph_optimized_phase1 (:851-890): per group, in id
+//     order, get_min_super_sets(label set, ids, avoid_self = true) with the default
+//     OptimizedBucket implementation (include/ung_build_config.h:83), restated from
+//     get_min_super_sets_optimized_bucket (:103-206) around the reference's
+//     TrieIndex::get_super_set_entrances (need_containment = true, the default of
+//     include/uni_nav_graph.h:284-285).
+// out_ptr needs G+2 entries (at most N+2); out_idx is written when out_cap is large
+// enough.  Returns the number of LNG edges (the caller retries with a larger out_cap
+// when it exceeds out_cap).
+int64_t ungref_trie_lng(uint64_t N, const uint32_t *lab_ptr, const uint32_t *lab_idx,
+                        uint32_t *point_group, uint32_t *G_out, uint32_t *out_ptr, uint32_t *out_idx,
+                        int64_t out_cap)
+{
+    using ANNS::IdxType;
+    using ANNS::LabelType;
+    using ANNS::TrieNode;
+    ANNS::TrieIndex trie;
+    IdxType new_group_id = 1;
+    std::vector<std::vector<LabelType>> set_of(1);
+    for (uint64_t i = 0; i < N; ++i) {
+        std::vector<LabelType> ls(lab_idx + lab_ptr[i], lab_idx + lab_ptr[i + 1]);
+        const IdxType g = trie.insert(ls, new_group_id);
+        if (g + 1 > set_of.size()) {
+            set_of.resize(g + 1);
+            set_of[g] = ls;
+        }
+        point_group[i] = g;
+    }
+    const uint32_t G = new_group_id - 1;
+    *G_out = G;
+
+    int64_t total = 0;
+    out_ptr[0] = out_ptr[1] = 0;
+    std::vector<std::shared_ptr<TrieNode>> candidates;
+    std::vector<TrieNode *> nodes;
+    std::vector<const std::vector<LabelType> *> min_sets;
+    std::vector<IdxType> row;
+    std::vector<std::vector<TrieNode *>> buckets;
+    for (uint32_t c = 1; c <= G; ++c) {
+        row.clear();
+        trie.get_super_set_entrances(set_of[c], candidates, true, true);
+        if (candidates.size() == 1) {
+            row.push_back(candidates[0]->group_id);
+        } else if (candidates.size() > 1) {
+            nodes.clear();
+            LabelType lo = candidates[0]->label_set_size, hi = lo;
+            for (const auto &sp : candidates) {
+                nodes.push_back(sp.get());
+                lo = std::min(lo, sp->label_set_size);
+                hi = std::max(hi, sp->label_set_size);
+            }
+            min_sets.clear();
+            auto consider = [&](const TrieNode *cand) {
+                const auto &ls = set_of[cand->group_id];
+                bool minimal = true;
+                if (cand->label_set_size > lo)
+                    for (const auto *m : min_sets)
+                        if (std::includes(ls.begin(), ls.end(), m->begin(), m->end())) {
+                            minimal = false;
+                            break;
+                        }
+                if (minimal) {
+                    row.push_back(cand->group_id);
+                    min_sets.push_back(&ls);
+                }
+            };
+            if (hi - lo <= 256) { // size buckets, each in entrance (BFS) order
+                buckets.assign(hi - lo + 1, {});
+                for (TrieNode *nd : nodes)
+                    buckets[nd->label_set_size - lo].push_back(nd);
+                for (const auto &b : buckets)
+                    for (const TrieNode *nd : b)
+                        consider(nd);
+            } else {
+                std::sort(nodes.begin(), nodes.end(), [](const TrieNode *a, const TrieNode *b) {
+                    return a->label_set_size < b->label_set_size;
+                });
+                for (const TrieNode *nd : nodes)
+                    consider(nd);
+            }
+        }
+        for (IdxType x : row) {
+            if (total < out_cap)
+                out_idx[total] = x;
+            ++total;
+        }
+        out_ptr[c + 1] = (uint32_t)total;
+    }
+    return total;
 }
 
 // Graph::save of the reference (include/graph.h:207-216) on a CSR adjacency.

@@ -1,8 +1,9 @@
 #!/usr/bin/env python3
 """Writes the golden fixtures of tests/golden/ from the reference's OWN compiled
-code: oracle/_ref/libungref.so = UNG/codes/src/distance.cpp + search_queue.cpp
-built from /root/reference by oracle/Makefile, driven by oracle/ref_driver.cpp
-(restating build_cross_edges_generate_cpu_exact_scan,
+code: oracle/_ref/libungref.so = UNG/codes/src/distance.cpp + search_queue.cpp +
+trie.cpp built from /root/reference by oracle/Makefile, driven by
+oracle/ref_driver.cpp (restating build_trie_and_divide_groups + the LNG phase 1
+with get_min_super_sets_optimized_bucket, build_cross_edges_generate_cpu_exact_scan,
 build_cross_edges_generate_additional (exact branch) and
 build_exact_topk_graph_for_points around those objects).
 
@@ -40,8 +41,13 @@ def make(cfg, name, k_cross=6, k_intra=32, intra_row_stride=1):
     X, lp, li = D.generate(cfg)
     st = F.UngBuildStage()
     st.prepare_inputs(X, lp, li)
-    ids, dists, size = ref.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, k_cross)
-    addl_ptr, addl_from, addl_to = ref.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx,
+    # groups and LNG rows from the reference's own TrieIndex (oracle/_ref); the product's
+    # reorder is only used to lay out the vectors group by group
+    G, pg, out_ptr, out_idx = ref.trie_lng(lp, li)
+    assert G == st.num_groups and np.array_equal(pg, st._point_group_old)
+    in_ptr, in_idx = F.in_neighbors(out_ptr, out_idx)
+    ids, dists, size = ref.cross_exact(st.base, st.group_begin, in_ptr, in_idx, k_cross)
+    addl_ptr, addl_from, addl_to = ref.additional_edges(st.base, st.group_begin, out_ptr, out_idx,
                                                         ids, k_cross)
     gids = st.mid_groups()
     rows_i, rows_d, grp_of_row, local_row = [], [], [], []
@@ -57,7 +63,7 @@ def make(cfg, name, k_cross=6, k_intra=32, intra_row_stride=1):
     keep = np.arange(0, intra_ids.shape[0], intra_row_stride)
     out = dict(
         x_sha256=np.array(sha(X)), labels_sha256=np.array(sha(lp, li)),
-        group_begin=st.group_begin, out_ptr=st.out_ptr, out_idx=st.out_idx,
+        group_begin=st.group_begin, out_ptr=out_ptr, out_idx=out_idx,
         cross_ids=ids, cross_dists=dists, cross_size=size,
         cross_sha256=np.array(sha(ids, dists, size)),
         addl_ptr=addl_ptr, addl_from=addl_from, addl_to=addl_to,

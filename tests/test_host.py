@@ -44,7 +44,9 @@ def test_lng_matches_oracle(oracle, seed, vocab, mmax, offset):
     sp, si = F.group_label_sets(lp, li, gb, n2o, G)
     op, oi = F.lng_build(sp, si, nthreads=4)
     rop, roi = oracle.min_supersets(sp, si)
-    assert np.array_equal(op, rop) and np.array_equal(oi, roi)
+    assert np.array_equal(op, rop)
+    for c in range(1, G + 1):  # same sets (the oracle lists each row by ascending id)
+        assert sorted(oi[op[c]: op[c + 1]].tolist()) == roi[rop[c]: rop[c + 1]].tolist()
 
 
 def test_lng_definition_small():
@@ -61,7 +63,53 @@ def test_lng_definition_small():
         for c, s in enumerate(sets, start=1):
             sup = [x for x, t in enumerate(sets, start=1) if set(s) < set(t)]
             mins = sorted(x for x in sup if not any(set(sets[y - 1]) < set(sets[x - 1]) for y in sup))
-            assert oi[op[c]: op[c + 1]].tolist() == mins
+            assert sorted(oi[op[c]: op[c + 1]].tolist()) == mins
+
+
+def _lng_of(lp, li, nthreads=4):
+    G, pg, gb, n2o = F.divide_groups(lp, li)
+    sp, si = F.group_label_sets(lp, li, gb, n2o, G)
+    op, oi = F.lng_build(sp, si, nthreads=nthreads)
+    return G, pg, sp, op, oi
+
+
+@pytest.mark.parametrize("name,n", [("cfg1", 10_000), ("cfg2", 50_000), ("cfg3", 6_000), ("cfg3", 40_000),
+                                    ("cfg4", 20_000), ("cfg5", 30_000)])
+def test_lng_order_matches_reference_trie(ref_oracle, name, n):
+    """Groups and LNG rows element by element, order included, against the reference's own
+    TrieIndex with the bucket loop of get_min_super_sets_optimized_bucket (oracle/_ref)."""
+    lp, li = D.synth_labels(D.scaled(D.CONFIGS[name], n))
+    G, pg, _, op, oi = _lng_of(lp, li)
+    rG, rpg, rop, roi = ref_oracle.trie_lng(lp, li)
+    assert G == rG and np.array_equal(pg, rpg)
+    assert np.array_equal(op, rop) and np.array_equal(oi, roi)
+
+
+@pytest.mark.parametrize("seed,vocab,mmax,lo,offset", [(11, 5, 4, 0, 0), (12, 40, 8, 0, 0), (13, 200, 3, 1, 0),
+                                                       (14, 12, 6, 0, 5000), (15, 3, 3, 0, 0), (16, 64, 5, 1, 60)])
+def test_lng_order_random_families(ref_oracle, seed, vocab, mmax, lo, offset):
+    """Random label families: empty label sets (lo = 0), deep sets, label ids past the
+    bitset path, ids that collide in small hash tables."""
+    rng = np.random.default_rng(seed)
+    _, lp, li = _labels(rng, 3000, vocab, mmax, lo, offset)
+    G, pg, _, op, oi = _lng_of(lp, li)
+    rG, rpg, rop, roi = ref_oracle.trie_lng(lp, li)
+    assert G == rG and np.array_equal(pg, rpg)
+    assert np.array_equal(op, rop) and np.array_equal(oi, roi)
+
+
+def test_lng_rows_in_size_buckets():
+    """Every row lists its minimal supersets by non-decreasing label-set size (the outer
+    order of the reference's bucket loop); a row sorted by id fails this on cfg3's labels."""
+    lp, li = D.synth_labels(D.scaled(D.CONFIGS["cfg3"], 20_000))
+    G, _, sp, op, oi = _lng_of(lp, li)
+    size = np.diff(sp.astype(np.int64))
+    unsorted_by_id = 0
+    for c in range(1, G + 1):
+        row = oi[op[c]: op[c + 1]].astype(np.int64)
+        assert (np.diff(size[row]) >= 0).all(), f"row {c} not in size order"
+        unsorted_by_id += int((np.diff(row) < 0).any())
+    assert unsorted_by_id > 0  # the order is not the id order
 
 
 def test_in_neighbors_transpose():
@@ -238,3 +286,29 @@ def test_graph_save_text(tmp_path, ref_oracle, cfg1_stage):
     F.graph_save_text(tmp_path / "a.txt", rp, ci, nthreads=4)
     ref_oracle.graph_save(tmp_path / "b.txt", rp, ci)
     assert (tmp_path / "a.txt").read_bytes() == (tmp_path / "b.txt").read_bytes()
+
+
+@pytest.mark.parametrize("name,n", [("cfg1", 10_000), ("cfg3", 6_000)])
+def test_graph_bytes_with_reference_lng(tmp_path, ref_oracle, name, n):
+    """The product's host pipeline (groups, reorder, LNG, CSR assembly, Graph::save)
+    writes the same bytes as the reference's own pieces: TrieIndex groups and LNG rows,
+    the exact cross and additional edges around its SearchQueue/distance, its Graph
+    container and Graph::save (all oracle/_ref).  The additional edges follow the LNG
+    row order, so this fails when a row is out of the reference's order."""
+    X, lp, li = D.generate(D.scaled(D.CONFIGS[name], n))
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    N = int(st.group_begin[-1])
+    cross, _, _ = ref_oracle.cross_exact(st.base, st.group_begin, st.in_ptr, st.in_idx, 6)
+    add = ref_oracle.additional_edges(st.base, st.group_begin, st.out_ptr, st.out_idx, cross, 6)
+    st.cross_flat_ids = cross
+    st.additional_edges = add
+    st.build_csr_adjacency()
+    st.save_graph(tmp_path / "product.txt")
+    G, _, rop, roi = ref_oracle.trie_lng(lp, li)
+    rip, rii = F.in_neighbors(rop, roi)
+    rcross, _, _ = ref_oracle.cross_exact(st.base, st.group_begin, rip, rii, 6)
+    radd = ref_oracle.additional_edges(st.base, st.group_begin, rop, roi, rcross, 6)
+    rp, ci = ref_oracle.assemble_graph(N, st.group_begin, None, None, False, rcross, 6, *radd)
+    ref_oracle.graph_save(tmp_path / "reference.txt", rp, ci)
+    assert (tmp_path / "product.txt").read_bytes() == (tmp_path / "reference.txt").read_bytes()
