@@ -75,6 +75,8 @@ SIGNATURES = {
     "ung_hip_group_knn_device": (_int, [_vp, _u32, _vp, _vp, _u32, _vp]),
     "ung_hip_group_result_device": (_int, [_vp, _vp, _vp, _vp]),
     "ung_hip_download_group": (_int, [_vp, _vp, _vp, _vp]),
+    "ung_hip_result_shape": (_int, [_vp, _int, C.POINTER(_u64), C.POINTER(_u32), C.POINTER(_u32)]),
+    "ung_hip_rescanned_rows": (_int, [_vp, _int, _vp, _u64, C.POINTER(_u64)]),
     "ung_hip_pack_anchor_rows": (_int, [_vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     "ung_hip_prune_group_graph": (_int, [_vp, _u32, _u32, _u32, C.c_float, _vp, _vp, _vp]),
     "ung_hip_cross_intra_begin": (_int, [_vp, _u32, _vp, _vp, _vp, _u32, _u32, _vp, _vp, _u32, _vp]),

@@ -2341,6 +2341,7 @@ struct ResultBufs {
     uint64_t rows = 0;
     uint32_t k = 0;
     bool valid = false;
+    std::vector<uint32_t> rescanned; // output rows of the last call that took the exact rescan
     void release()
     {
         ids.release();
@@ -2348,6 +2349,7 @@ struct ResultBufs {
         size.release();
         rows = 0;
         valid = false;
+        rescanned.clear();
     }
 };
 
@@ -2793,8 +2795,15 @@ int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
             HIPCHECK(hipGetLastError());
         }
     }
+    std::vector<uint2> flagged_host(nflag);
+    if (nflag > 0)
+        HIPCHECK(hipMemcpyAsync(flagged_host.data(), ws.flagged.p, nflag * sizeof(uint2), hipMemcpyDeviceToHost,
+                                ws.stream));
     HIPCHECK(hipEventRecord(ws.ev[3], ws.stream));
     HIPCHECK(hipEventSynchronize(ws.ev[3]));
+    for (const uint2 &f : flagged_host)
+        res.rescanned.push_back(pl.jobs[f.x].out_row + f.y);
+    std::sort(res.rescanned.begin(), res.rescanned.end());
     if (st) {
         float a = 0, b = 0, c = 0;
         HIPCHECK(hipEventElapsedTime(&a, ws.ev[0], ws.ev[1]));
@@ -2920,12 +2929,27 @@ int group_prepare_result(ung_hip_ctx *ctx, const Plan &pl, uint32_t list_k);
 int group_complete(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t list_k);
 int check_not_pending(ung_hip_ctx *ctx, const char *who);
 
+// After a failed call: waits for whatever the workspaces still have in flight, so no
+// buffer is reused or freed under a running kernel.  The failed call's result stays
+// invalid (cross_prepare_result / group_prepare_result cleared its flag before anything
+// was enqueued).  Errors of the waits are ignored: the call's own error is reported.
+void drain_after_failure(ung_hip_ctx *ctx)
+{
+    for (Workspace &w : ctx->ws) {
+        if (w.stream)
+            (void)hipStreamSynchronize(w.stream);
+        if (w.upload)
+            (void)hipStreamSynchronize(w.upload);
+    }
+}
+
 // Result rows of a cross call, initialised (padding) on the first workspace's stream.
 int cross_prepare_result(ung_hip_ctx *ctx, uint32_t k)
 {
     int rc;
     ResultBufs &res = ctx->cross;
     res.valid = false;
+    res.rescanned.clear();
     if ((rc = res.ids.ensure(ctx->N * k)) || (rc = res.dist.ensure(ctx->N * k)) || (rc = res.size.ensure(ctx->N)))
         return rc;
     res.rows = ctx->N;
@@ -2958,8 +2982,10 @@ int cross_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, cons
         return rc;
     if (st)
         st->plan_ms += ms_since(t0);
-    if ((rc = cross_prepare_result(ctx, k)) || (rc = run_plan(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
+    if ((rc = cross_prepare_result(ctx, k)) || (rc = run_plan(ctx, ctx->ws[0], pl, k, ctx->cross, st))) {
+        drain_after_failure(ctx);
         return rc;
+    }
     HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
     ctx->cross.valid = true;
     if (st)
@@ -2990,27 +3016,36 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         return rc;
     if (st)
         st->plan_ms += ms_since(t0);
-    if ((rc = cross_prepare_result(ctx, k)) || (rc = plan_launch(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
-        return rc;
-    // the group call is planned while the cross kernels run
+    // both calls are planned and validated before anything is enqueued, so an invalid
+    // group list leaves no cross work in flight
     ctx->intra_stats = ung_hip_stats{};
     ctx->intra_t0 = clk::now();
     plan_reset(ctx->intra_plan);
     if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, ctx->intra_plan)))
         return rc;
     ctx->intra_stats.plan_ms += ms_since(ctx->intra_t0);
+    // the group call's kernels start when the cross select ends: they fill the chip while
+    // the cross merge (memory-bound), rescan and the caller's next steps run
+    if ((rc = cross_prepare_result(ctx, k)) || (rc = plan_launch(ctx, ctx->ws[0], pl, k, ctx->cross, st)) ||
+        (rc = group_prepare_result(ctx, ctx->intra_plan, list_k)) ||
+        (rc = plan_launch(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats,
+                          ctx->ws[0].ev[1]))) {
+        drain_after_failure(ctx);
+        return rc;
+    }
     // from here the group call is in flight on the second workspace until intra_end
     ctx->intra_list_k = list_k;
     ctx->intra_pending = true;
-    // the group call's kernels start when the cross select ends: they fill the chip while
-    // the cross merge (memory-bound), rescan and the caller's next steps run
-    if ((rc = group_prepare_result(ctx, ctx->intra_plan, list_k)) ||
-        (rc = plan_launch(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats,
-                          ctx->ws[0].ev[1])))
+    rc = plan_finish(ctx, ctx->ws[0], pl, k, ctx->cross, st);
+    if (rc == UNG_HIP_OK && hipStreamSynchronize(ctx->ws[0].stream) != hipSuccess) {
+        set_error("ung_hip_cross_intra_begin: stream synchronisation failed");
+        rc = UNG_HIP_EDEVICE;
+    }
+    if (rc) { // the group call is abandoned with the cross call (its lists stay invalid)
+        drain_after_failure(ctx);
+        ctx->intra_pending = false;
         return rc;
-    if ((rc = plan_finish(ctx, ctx->ws[0], pl, k, ctx->cross, st)))
-        return rc;
-    HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
+    }
     ctx->cross.valid = true;
     if (st)
         st->wall_ms += ms_since(t0);
@@ -3029,8 +3064,10 @@ int intra_end(ung_hip_ctx *ctx, ung_hip_stats *st)
     ctx->intra_pending = false;
     const uint32_t list_k = ctx->intra_list_k;
     if ((rc = plan_finish(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats)) ||
-        (rc = group_complete(ctx, ctx->ws[1], ctx->intra_plan, list_k)))
+        (rc = group_complete(ctx, ctx->ws[1], ctx->intra_plan, list_k))) {
+        drain_after_failure(ctx);
         return rc;
+    }
     ctx->intra_stats.wall_ms += ms_since(ctx->intra_t0);
     if (st) {
         st->wall_ms += ctx->intra_stats.wall_ms;
@@ -3108,6 +3145,7 @@ int group_prepare_result(ung_hip_ctx *ctx, const Plan &pl, uint32_t list_k)
     int rc;
     ResultBufs &res = ctx->group;
     res.valid = false;
+    res.rescanned.clear();
     if ((rc = res.ids.ensure(std::max<uint64_t>(pl.rows * list_k, 1))) ||
         (rc = res.dist.ensure(std::max<uint64_t>(pl.rows * list_k, 1))) ||
         (rc = res.size.ensure(std::max<uint64_t>(pl.rows, 1))))
@@ -3160,12 +3198,11 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         return rc;
     if (st)
         st->plan_ms += ms_since(t0);
-    if ((rc = group_prepare_result(ctx, pl, list_k)))
+    if ((rc = group_prepare_result(ctx, pl, list_k)) || (rc = run_plan(ctx, ctx->ws[0], pl, list_k, ctx->group, st)) ||
+        (rc = group_complete(ctx, ctx->ws[0], pl, list_k))) {
+        drain_after_failure(ctx);
         return rc;
-    if ((rc = run_plan(ctx, ctx->ws[0], pl, list_k, ctx->group, st)))
-        return rc;
-    if ((rc = group_complete(ctx, ctx->ws[0], pl, list_k)))
-        return rc;
+    }
     if (st)
         st->wall_ms += ms_since(t0);
     return UNG_HIP_OK;
@@ -3685,6 +3722,50 @@ int ung_hip_group_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **di
         *dist_dev = ctx->group.dist.p;
     if (rows)
         *rows = ctx->group.rows;
+    return UNG_HIP_OK;
+}
+
+int ung_hip_result_shape(ung_hip_ctx *ctx, int which, uint64_t *rows, uint32_t *k, uint32_t *n_groups)
+{
+    clear_error();
+    if (!ctx || (which != 0 && which != 1)) {
+        set_error("ung_hip_result_shape: null context or which not 0/1");
+        return UNG_HIP_EINVAL;
+    }
+    const ResultBufs &res = which == 0 ? ctx->cross : ctx->group;
+    if (!res.valid) {
+        set_error("ung_hip_result_shape: no %s result on the device", which == 0 ? "cross-edge" : "group kNN");
+        return UNG_HIP_ESTATE;
+    }
+    if (rows)
+        *rows = res.rows;
+    if (k)
+        *k = res.k;
+    if (n_groups)
+        *n_groups = which == 0 ? 0u : (uint32_t)ctx->group_jobs.size();
+    return UNG_HIP_OK;
+}
+
+int ung_hip_rescanned_rows(ung_hip_ctx *ctx, int which, uint32_t *rows, uint64_t capacity, uint64_t *n_rows)
+{
+    clear_error();
+    if (!ctx || (which != 0 && which != 1) || !n_rows) {
+        set_error("ung_hip_rescanned_rows: null context/n_rows or which not 0/1");
+        return UNG_HIP_EINVAL;
+    }
+    const ResultBufs &res = which == 0 ? ctx->cross : ctx->group;
+    if (!res.valid) {
+        set_error("ung_hip_rescanned_rows: no %s result on the device", which == 0 ? "cross-edge" : "group kNN");
+        return UNG_HIP_ESTATE;
+    }
+    *n_rows = res.rescanned.size();
+    if (res.rescanned.size() > capacity || (!rows && !res.rescanned.empty())) {
+        set_error("ung_hip_rescanned_rows: capacity %llu < %zu rows", (unsigned long long)capacity,
+                  res.rescanned.size());
+        return UNG_HIP_EINVAL;
+    }
+    if (!res.rescanned.empty())
+        std::memcpy(rows, res.rescanned.data(), res.rescanned.size() * sizeof(uint32_t));
     return UNG_HIP_OK;
 }
 

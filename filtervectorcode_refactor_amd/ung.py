@@ -127,7 +127,37 @@ class HipContext:
         self._keep = None
         return st.as_dict()
 
-    def download_cross(self, N: int, k: int):
+    def result_shape(self, which: int):
+        """(rows, k, n_groups) of the resident cross rows (which=0) or group lists (which=1)
+        (ung_hip_result_shape); raises when there is none."""
+        rows, k, ng = C.c_uint64(), C.c_uint32(), C.c_uint32()
+        check(self.lib.ung_hip_result_shape(self.h, which, C.byref(rows), C.byref(k), C.byref(ng)))
+        return int(rows.value), int(k.value), int(ng.value)
+
+    def rescanned_rows(self, which: int) -> np.ndarray:
+        """Output rows of the last cross (which=0) or group (which=1) call that took the exact
+        rescan, ascending (ung_hip_rescanned_rows)."""
+        n = C.c_uint64(0)
+        rc = self.lib.ung_hip_rescanned_rows(self.h, which, None, 0, C.byref(n))
+        if rc == _lib.UNG_HIP_OK:
+            return np.zeros(0, np.uint32)
+        if rc != _lib.UNG_HIP_EINVAL or n.value == 0:
+            check(rc)
+        rows = np.empty(int(n.value), np.uint32)
+        check(self.lib.ung_hip_rescanned_rows(self.h, which, ptr(rows), rows.shape[0], C.byref(n)))
+        return rows
+
+    def _checked_shape(self, which, rows=None, k=None, n_groups=None):
+        """The resident shape; a caller-given size that differs from it raises ValueError
+        (the library writes the resident shape, not the caller's)."""
+        r, kk, ng = self.result_shape(which)
+        for name, want, got in (("rows", rows, r), ("k", k, kk), ("n_groups", n_groups, ng)):
+            if want is not None and int(want) != got:
+                raise ValueError(f"{name}={want} does not match the resident result ({name}={got})")
+        return r, kk, ng
+
+    def download_cross(self, N: int | None = None, k: int | None = None):
+        N, k, _ = self._checked_shape(0, N, k)
         ids = np.empty((N, k), np.uint32)
         dist = np.empty((N, k), np.float32)
         size = np.empty(N, np.int32)
@@ -135,8 +165,9 @@ class HipContext:
         check(self.lib.ung_hip_download_cross(self.h, ptr(ids), ptr(dist), ptr(size), C.byref(st)))
         return ids, dist, size, st.as_dict()
 
-    def download_group(self, rows: int, list_k: int):
+    def download_group(self, rows: int | None = None, list_k: int | None = None):
         """The resident lists of the last group kNN call (ung_hip_download_group)."""
+        rows, list_k, _ = self._checked_shape(1, rows, list_k)
         ids = np.empty((rows, list_k), np.uint32)
         dist = np.empty((rows, list_k), np.float32)
         st = Stats()
@@ -186,9 +217,10 @@ class HipContext:
                                                 list_k, C.byref(st)))
         return st.as_dict()
 
-    def pack_anchor_rows(self, rows: int, n_groups: int, tagore_k: int, final_degree: int,
+    def pack_anchor_rows(self, rows: int | None, n_groups: int | None, tagore_k: int, final_degree: int,
                          head_keep: int, anchor_tail: int = 1, anchor_slots: int = 0,
                          bidir_anchor: int = 0):
+        rows, _, n_groups = self._checked_shape(1, rows, None, n_groups)
         stride = final_degree + 1
         graph = np.empty((rows, stride), np.uint32)
         entries = np.empty(max(n_groups, 1), np.uint32)
@@ -198,10 +230,11 @@ class HipContext:
                                                 C.byref(st)))
         return graph, entries[:n_groups], st.as_dict()
 
-    def prune_group_graph(self, rows: int, n_groups: int, forward_cap: int, reverse_cap: int,
+    def prune_group_graph(self, rows: int | None, n_groups: int | None, forward_cap: int, reverse_cap: int,
                           final_degree: int, alpha: float):
         """FastGrnnd-style prune of the last group_knn(_device) lists (ung_hip_prune_group_graph):
         rows [rows x (final_degree+1)] = [count, local ids, padding], entry points, stats."""
+        rows, _, n_groups = self._checked_shape(1, rows, None, n_groups)
         stride = final_degree + 1
         graph = np.empty((rows, stride), np.uint32)
         entries = np.empty(max(n_groups, 1), np.uint32)

@@ -175,6 +175,22 @@ int ung_hip_group_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **di
 int ung_hip_download_group(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist,
                            ung_hip_stats *st);
 
+/* Shape of a resident result, for sizing the host buffers of the downloads, the packed
+ * rows and the pruned rows: which = 0 the cross-edge rows (rows = N, k = the call's k,
+ * n_groups = 0), which = 1 the group kNN lists of the last group call (rows = sum n,
+ * k = list_k, n_groups = its group count).  Output pointers may be NULL.
+ * UNG_HIP_ESTATE when there is no such result.  No counterpart in the reference, whose
+ * results are std::vectors that carry their sizes. */
+int ung_hip_result_shape(ung_hip_ctx *ctx, int which, uint64_t *rows, uint32_t *k, uint32_t *n_groups);
+
+/* Output rows of the last cross-edge call (which = 0: point ids) or group kNN call
+ * (which = 1: packed row indices) whose MFMA pre-selection could not be certified and
+ * that were rescanned exactly (ung_hip_stats::fallback_rows of that call), ascending.
+ * *n_rows receives the count; UNG_HIP_EINVAL (nothing written) when capacity is smaller.
+ * Diagnostic for parity checks; the reference's sampled verifier
+ * (src/gpu_cross_edge_verify.cuh:38-203) has no such list. */
+int ung_hip_rescanned_rows(ung_hip_ctx *ctx, int which, uint32_t *rows, uint64_t capacity, uint64_t *n_rows);
+
 /* Exact-anchor row packing of the last ung_hip_group_knn(_device) result, on the
  * device.  Same rows as batched_exact_knn_graph_kernel's epilogue
  * (src/tagore_graph_builder.cu:727-794) with its defaults from
@@ -218,8 +234,8 @@ int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t r
 /* Synchronise the context's stream (for callers timing the device variants). */
 int ung_hip_synchronize(ung_hip_ctx *ctx);
 
-/* Device-side self test of the fp32 MFMA fragment layout the kernels rely on
- * (diagnostic, no counterpart in the reference).  *max_abs_err receives the
+/* Device-side self test of the bf16 MFMA fragment layout the kernels rely on
+ * (v_mfma_f32_32x32x16_bf16; diagnostic, no counterpart in the reference).  *max_abs_err receives the
  * largest deviation from a host-computed product; returns 0 when it ran. */
 int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err);
 
@@ -276,9 +292,14 @@ int ung_group_label_sets(uint64_t N, const uint32_t *lab_ptr, const uint32_t *la
 /* Label navigating graph: out(C) = minimum proper supersets among the groups.
  * Replaces build_label_nav_graph phase 1 (src/uni_nav_graph_label_graph.cpp:851-911,
  * get_min_super_sets :45-206 with TrieIndex::get_super_set_entrances
- * src/trie.cpp:78-143).  out_ptr[G+2]; out_idx capacity out_cap (rows ascending
- * group id).  *n_edges receives the edge count; returns UNG_HIP_EINVAL with
- * *n_edges set to the needed capacity when out_cap is too small. */
+ * src/trie.cpp:78-143).  out_ptr[G+2]; out_idx capacity out_cap.  Each row is in the
+ * reference's order: by label-set size, and within one size in the discovery order of
+ * the reference's trie walk (get_min_super_sets_optimized_bucket,
+ * src/uni_nav_graph_label_graph.cpp:103-206, whose groups are inserted in first-appearance
+ * order); rows whose candidate label-set sizes span more than 256 are sorted by the
+ * reference with an unstable std::sort and keep the walk order here.  *n_edges receives
+ * the edge count; returns UNG_HIP_EINVAL with *n_edges set to the needed capacity when
+ * out_cap is too small. */
 int ung_lng_build(uint32_t G, const uint32_t *set_ptr, const uint32_t *set_idx,
                   uint32_t *out_ptr, uint32_t *out_idx, uint64_t out_cap, uint64_t *n_edges,
                   int nthreads);

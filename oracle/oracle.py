@@ -101,6 +101,8 @@ class Oracle:
         L = C.CDLL(path)
         L.ungo_l2.restype = C.c_float
         L.ungo_l2.argtypes = [_f32p, _f32p, C.c_uint32]
+        L.ungo_l2_pairs.restype = None
+        L.ungo_l2_pairs.argtypes = [_f32p, C.c_uint32, _u32p, _u32p, C.c_uint64, _f32p]
         L.ungo_l2_f64.restype = C.c_double
         L.ungo_l2_f64.argtypes = [_f32p, _f32p, C.c_uint32]
         L.ungo_queue_insert.restype = C.c_int
@@ -137,6 +139,14 @@ class Oracle:
     def l2(self, a, b) -> float:
         a, b = _f32(a), _f32(b)
         return float(self.lib.ungo_l2(a, b, a.shape[0]))
+
+    def l2_pairs(self, X, a, b):
+        """ungo_l2 of the row pairs (X[a[i]], X[b[i]]); +inf where b[i] is UINT32_MAX."""
+        X = _f32(X)
+        a, b = _u32(a).reshape(-1), _u32(b).reshape(-1)
+        out = np.empty(a.shape[0], np.float32)
+        self.lib.ungo_l2_pairs(X, X.shape[1], a, b, a.shape[0], out)
+        return out
 
     def l2_f64(self, a, b) -> float:
         a, b = _f32(a), _f32(b)

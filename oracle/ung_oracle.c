@@ -68,6 +68,14 @@ float ungo_l2(const float *a, const float *b, uint32_t dim)
     return (s[0] + s[1]) + (s[2] + s[3]);
 }
 
+void ungo_l2_pairs(const float *X, uint32_t dim, const uint32_t *a, const uint32_t *b, uint64_t n, float *out)
+{
+#pragma omp parallel for schedule(static, 4096)
+    for (int64_t i = 0; i < (int64_t)n; ++i)
+        out[i] = b[i] == 0xFFFFFFFFu ? INFINITY
+                                     : ungo_l2(X + (size_t)a[i] * dim, X + (size_t)b[i] * dim, dim);
+}
+
 double ungo_l2_f64(const float *a, const float *b, uint32_t dim)
 {
     double s = 0.0;

@@ -27,6 +27,11 @@ extern "C" {
  * horizontal adds: (s0+s1)+(s2+s3). */
 float ungo_l2(const float *a, const float *b, uint32_t dim);
 
+/* ungo_l2 of n row pairs of X [* x dim]: out[i] = ungo_l2(X[a[i]], X[b[i]]) (OpenMP);
+ * pairs with b[i] == UINT32_MAX give +inf.  Used by tests to check every reported
+ * distance of a large result bit for bit. */
+void ungo_l2_pairs(const float *X, uint32_t dim, const uint32_t *a, const uint32_t *b, uint64_t n, float *out);
+
 /* Double-precision squared L2 (no relation to the reference; used by tests as
  * an independent brute-force check of ungo_l2). */
 double ungo_l2_f64(const float *a, const float *b, uint32_t dim);

@@ -1,0 +1,223 @@
+"""GPU parity on every BASELINE configuration (run on an MI355X, through the C ABI).
+
+* cfg1 (10k x 128) and a 6,000-point sample of cfg3's generator (d = 384): the HIP path
+  against the golden fixtures written by the reference's own compiled code
+  (tests/golden/*_ref.npz, made by tests/golden/make_golden.py): group ranges and LNG rows
+  (the reference's trie order), cross ids / distances / sizes, additional edges, every
+  intra list (digest) and the stored intra rows -- all bit-exact.
+* cfg3 (1M x 384), cfg4 (2M x 768: its split base set is above 4 GiB, so the wide load
+  mode runs) and cfg5 (10M x 128: above 4 GiB) at full size:
+  - every cross row: size = min(k, |union|), padding, (dist, id) order, every id inside
+    the row's minimum-superset union, and every distance bit-exact against the reference's
+    summation order (oracle ungo_l2_pairs, pinned against the compiled reference);
+  - every row the certificate sent to the exact rescan, plus a large random sample of
+    rows, bit-exact against the reference's compiled distance + SearchQueue scan
+    (oracle/_ref, else the plain-C oracle);
+  - the additional edges of a sample of groups against the oracle fed the GPU's cross rows;
+  - every intra row (mid groups, K = 32): size, local ids, no self, (dist, id) order,
+    distances bit-exact; every rescanned intra row and a sample of groups bit-exact.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+
+import filtervectorcode_refactor_amd as F
+from filtervectorcode_refactor_amd import datasets as D
+from conftest import load_golden
+from test_gpu_parity import _assert_rows_equal
+
+pytestmark = pytest.mark.gpu
+NONE = 0xFFFFFFFF
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def _checker(oracle):
+    from oracle import RefOracle, ref_available
+    return RefOracle() if ref_available() else oracle
+
+
+# ------------------------------------------------------------------ golden fixtures
+@pytest.mark.parametrize("fixture,cfg_name,n", [("cfg1_ref.npz", "cfg1", 10_000), ("cfg3_6k_ref.npz", "cfg3", 6_000)])
+def test_golden_fixture(fixture, cfg_name, n):
+    g = load_golden(fixture)
+    X, lp, li = D.generate(D.scaled(D.CONFIGS[cfg_name], n))
+    assert _sha(X) == str(g["x_sha256"]) and _sha(lp, li) == str(g["labels_sha256"]), "generator drift"
+    st = F.UngBuildStage()
+    st.prepare_inputs(X, lp, li)
+    for key in ("group_begin", "out_ptr", "out_idx"):
+        assert np.array_equal(getattr(st, key), g[key]), f"{fixture}: {key} differs from the reference's"
+    _say(f"golden {fixture}: {st.num_groups} groups, {len(st.out_idx)} LNG edges")
+    with F.HipContext(0) as ctx:
+        ctx.prepare_vectors(st.base)
+        ids, dist, size, _ = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, 6)
+        _assert_rows_equal(ids, dist, size, g["cross_ids"], g["cross_dists"], g["cross_size"], f"{fixture} cross")
+        ep, ef, et, _ = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, 6)
+        assert np.array_equal(ep, g["addl_ptr"]), f"{fixture}: additional edge counts"
+        assert np.array_equal(ef, g["addl_from"]) and np.array_equal(et, g["addl_to"]), f"{fixture}: additional edges"
+        gids = g["intra_groups"].astype(np.int64)
+        begins = st.group_begin[gids].astype(np.uint32)
+        sizes = (st.group_begin[gids + 1] - st.group_begin[gids]).astype(np.uint32)
+        kids, kdist, _ = ctx.group_knn(begins, sizes, int(g["intra_k"]))
+        rows = g["intra_rows"].astype(np.int64)
+        assert np.array_equal(kids[rows].astype(np.uint16), g["intra_ids"]), f"{fixture}: stored intra rows"
+        assert np.array_equal(kdist[rows].view(np.uint32), g["intra_dists"].view(np.uint32))
+        assert _sha(kids, kdist) == str(g["intra_sha256"]), f"{fixture}: intra lists differ from the reference's"
+
+
+# ------------------------------------------------------------------ full-size configs
+def _union_sizes(st):
+    sizes = np.diff(st.group_begin.astype(np.int64))[1:]
+    cnt = np.diff(st.out_ptr.astype(np.int64))[1:]
+    union = np.zeros(st.num_groups + 1, np.int64)
+    src = np.repeat(np.arange(1, st.num_groups + 1, dtype=np.int64), cnt)
+    np.add.at(union, src, sizes[st.out_idx.astype(np.int64) - 1])
+    return union
+
+
+def _check_rows(oracle, X, src_rows, ids, dist, count, chunk=1 << 19):
+    """Every row r: the first count[r] entries are valid, the rest padding (UINT32_MAX,
+    +inf); valid entries in strict (dist, id) order; every distance equal bit for bit to
+    the reference's summation order between X[src_rows[r]] and X[ids[r, j]] (ids global)."""
+    k = ids.shape[1]
+    for r0 in range(0, ids.shape[0], chunk):
+        r1 = min(ids.shape[0], r0 + chunk)
+        I, Dd, S = ids[r0:r1], dist[r0:r1], count[r0:r1]
+        valid = np.arange(k)[None, :] < S[:, None]
+        assert ((I == NONE) == ~valid).all(), f"rows {r0}..{r1}: padding"
+        d0, d1, i0, i1 = Dd[:, :-1], Dd[:, 1:], I[:, :-1], I[:, 1:]
+        assert ((d0 < d1) | ((d0 == d1) & (i0 < i1)) | ~valid[:, 1:]).all(), f"rows {r0}..{r1}: (dist, id) order"
+        a = np.repeat(src_rows[r0:r1].astype(np.uint32), k)
+        exact = oracle.l2_pairs(X, a, I.reshape(-1)).reshape(I.shape)
+        bad = np.nonzero((exact.view(np.uint32) != Dd.view(np.uint32)).any(axis=1))[0]
+        assert bad.size == 0, f"{bad.size} rows with a distance not bit-exact, first {r0 + bad[0]}"
+
+
+def _full_size(cfg_name, oracle, n_cross_sample, n_intra_groups, addl_budget_dims):
+    cfg = D.CONFIGS[cfg_name]
+    rng = np.random.default_rng(17)
+    _say(f"{cfg_name} full: generate {cfg.n} x {cfg.dim}")
+    X, lp, li = D.generate(cfg)
+    st = F.UngBuildStage(num_cross_edges=cfg.k_cross, max_degree=cfg.k_intra)
+    st.prepare_inputs(X, lp, li)
+    del X
+    N, G, k, K = st.base.shape[0], st.num_groups, cfg.k_cross, cfg.k_intra
+    chk = _checker(oracle)
+    ctx = st.ctx
+    ctx.prepare_vectors(st.base)
+    _say(f"{cfg_name} full: cross ({G} groups, {len(st.out_idx)} LNG edges)")
+    ids, dist, size, stats = ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, k)
+    _say(f"{cfg_name} full: cross done, select {stats['select_ms']:.1f} ms, {stats['fallback_rows']} rescanned")
+    assert stats["fallback_rows"] <= N // 1000
+    pg = st.new_vec_id_to_group_id
+    union = _union_sizes(st)
+    assert np.array_equal(size, np.minimum(k, union[pg]).astype(np.int32)), "row sizes"
+    # every id inside the union of the row's minimum supersets
+    cnt = np.diff(st.out_ptr.astype(np.int64))[1:]
+    keys = np.sort(np.repeat(np.arange(1, G + 1, dtype=np.int64), cnt) * (G + 1) + st.out_idx.astype(np.int64))
+    for r0 in range(0, N, 1 << 20):
+        r1 = min(N, r0 + (1 << 20))
+        I = ids[r0:r1]
+        v = I != NONE
+        rows = np.broadcast_to(np.arange(r0, r1, dtype=np.int64)[:, None], I.shape)[v]
+        key = pg[rows].astype(np.int64) * (G + 1) + pg[I[v].astype(np.int64)].astype(np.int64)
+        pos = np.minimum(np.searchsorted(keys, key), keys.size - 1)
+        assert (keys[pos] == key).all(), f"rows {r0}..{r1}: an id outside its row's union"
+    _say(f"{cfg_name} full: distances of every cross row")
+    _check_rows(oracle, st.base, np.arange(N, dtype=np.uint32), ids, dist, size)
+    # every rescanned row and a random sample, bit-exact against the reference's scan
+    rescanned = ctx.rescanned_rows(0)
+    assert rescanned.size == stats["fallback_rows"]
+    eligible = np.nonzero(union[pg] > 0)[0]
+    sample = rng.choice(eligible, size=min(n_cross_sample, eligible.size), replace=False)
+    q = np.union1d(sample, rescanned).astype(np.uint32)
+    _say(f"{cfg_name} full: {q.size} rows ({rescanned.size} rescanned) against the reference scan")
+    res = chk.cross_exact_points(st.base, st.group_begin, pg, st.out_ptr, st.out_idx, q, k)
+    _assert_rows_equal(ids[q], dist[q], None, res[0], res[1], None, f"{cfg_name} full cross rows")
+
+    # additional edges of a sample of groups (each group's list depends only on its own
+    # cross rows and LNG row, so the oracle gets an LNG with only those rows)
+    ep, ef, et, ast = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, k)
+    _say(f"{cfg_name} full: {ef.size} additional edges, {ast['rows']} query rows")
+    sizes = np.diff(st.group_begin.astype(np.int64))[1:]
+    xs = sizes[pg[et].astype(np.int64) - 1] if et.size else np.zeros(0, np.int64)
+    cost = np.zeros(G + 2, np.float64)  # oracle work of a group's list: |X| * d per scanned row
+    if et.size:
+        grp = np.repeat(np.arange(G + 2), np.diff(np.concatenate([ep.astype(np.int64), [ep[-1]]])))[: et.size]
+        np.add.at(cost, grp, xs * cfg.dim / np.minimum(xs, k // 2))
+    has_out = np.nonzero(cnt > 0)[0] + 1
+    order = rng.permutation(has_out)
+    pick, spent = [], 0.0
+    for c in order:
+        if spent + cost[c] > addl_budget_dims:
+            continue
+        pick.append(int(c))
+        spent += cost[c]
+        if len(pick) >= 4000:
+            break
+    pick = np.sort(np.array(pick, np.int64))
+    keep = np.zeros(G + 1, bool)
+    keep[pick] = True
+    rcnt = cnt * keep[1:]
+    rop = np.zeros(G + 2, np.uint32)
+    rop[2:] = np.cumsum(rcnt)
+    roi = np.concatenate([st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]] for c in pick]).astype(np.uint32)
+    _say(f"{cfg_name} full: additional edges of {pick.size} groups against the oracle ({spent:.2e} dims)")
+    wp, wf, wt = oracle.additional_edges(st.base, st.group_begin, rop, roi, ids, k)
+    n_with = 0
+    for c in pick:
+        a0, a1, b0, b1 = int(ep[c]), int(ep[c + 1]), int(wp[c]), int(wp[c + 1])
+        assert np.array_equal(ef[a0:a1], wf[b0:b1]) and np.array_equal(et[a0:a1], wt[b0:b1]), f"group {c}"
+        n_with += a1 > a0
+    _say(f"{cfg_name} full: {n_with} of the sampled groups have additional edges")
+    del ids, dist, size
+
+    # intra lists of every mid group
+    gids = st.mid_groups().astype(np.int64)
+    begins = st.group_begin[gids].astype(np.int64)
+    gsz = (st.group_begin[gids + 1] - st.group_begin[gids]).astype(np.int64)
+    _say(f"{cfg_name} full: intra kNN of {gids.size} mid groups")
+    kids, kdist, kst = ctx.group_knn(begins.astype(np.uint32), gsz.astype(np.uint32), K)
+    assert kst["fallback_rows"] <= max(1, kids.shape[0] // 1000)
+    row_grp = np.repeat(np.arange(gids.size), gsz)
+    row_local = np.arange(kids.shape[0], dtype=np.int64) - np.repeat(np.cumsum(gsz) - gsz, gsz)
+    n_row = gsz[row_grp]
+    v = kids != NONE
+    assert (kids[v] < np.broadcast_to(n_row[:, None], kids.shape)[v]).all(), "intra: local id out of range"
+    assert (kids[v] != np.broadcast_to(row_local[:, None], kids.shape)[v]).all(), "intra: self in a list"
+    glob = np.where(v, kids.astype(np.int64) + begins[row_grp][:, None], NONE).astype(np.uint32)
+    _check_rows(oracle, st.base, (begins[row_grp] + row_local).astype(np.uint32), glob, kdist,
+                np.minimum(K, n_row - 1))
+    rescanned = ctx.rescanned_rows(1)
+    assert rescanned.size == kst["fallback_rows"]
+    pick_g = set(rng.choice(gids.size, size=min(n_intra_groups, gids.size), replace=False).tolist())
+    pick_g |= set(row_grp[rescanned].tolist())
+    _say(f"{cfg_name} full: {len(pick_g)} groups ({rescanned.size} rescanned rows) against the reference")
+    starts = np.cumsum(gsz) - gsz
+    for gi in sorted(pick_g):
+        b, n, r0 = int(begins[gi]), int(gsz[gi]), int(starts[gi])
+        o_i, o_d = chk.intra_exact(st.base, b, n, K)
+        _assert_rows_equal(kids[r0: r0 + n], kdist[r0: r0 + n], None, o_i, o_d, None, f"{cfg_name} intra {gi}")
+    st.close()
+
+
+def test_cfg3_full_size(oracle):
+    _full_size("cfg3", oracle, n_cross_sample=50_000, n_intra_groups=40, addl_budget_dims=2e10)
+
+
+def test_cfg4_full_size(oracle):
+    _full_size("cfg4", oracle, n_cross_sample=20_000, n_intra_groups=30, addl_budget_dims=2e10)
+
+
+def test_cfg5_full_size(oracle):
+    _full_size("cfg5", oracle, n_cross_sample=10_000, n_intra_groups=30, addl_budget_dims=2e10)

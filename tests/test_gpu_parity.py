@@ -384,14 +384,20 @@ def test_cross_intra_overlapped_equals_sequential(ctx, oracle):
         for a, w in zip(got_add[:3], want_add[:3]):
             assert np.array_equal(a, w)
         assert np.array_equal(check_ids, g_ids) and np.array_equal(check_dist, g_dist)
-    # an invalid group list is refused (the cross kernels it already started finish on
-    # their own); the next overlapped call gives the same rows
+    # an invalid group list or list_k is refused by the host checks before anything is
+    # enqueued (no call is left in flight); the next overlapped call gives the same rows
     bad_n = n.copy()
     bad_n[0] = 0
-    with pytest.raises(F.UngHipError):
-        ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, 6, b, bad_n, 32)
-    with pytest.raises(F.UngHipError):
-        ctx.intra_end()
+    for bad_sizes, bad_k in ((bad_n, 32), (n, 0), (n, 65)):
+        with pytest.raises(F.UngHipError) as e:
+            ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, 6, b, bad_sizes, bad_k)
+        assert e.value.code == -1
+        with pytest.raises(F.UngHipError) as e:
+            ctx.intra_end()
+        assert e.value.code == -3
+    # the resident cross rows of the last complete call are still there
+    ids, dist, size, _ = ctx.download_cross(st.base.shape[0], 6)
+    assert np.array_equal(ids, c_ids) and np.array_equal(dist, c_dist) and np.array_equal(size, c_size)
     ctx.cross_intra_begin(st.group_begin, st.out_ptr, st.out_idx, 6, b, n, 32)
     ids, dist, size, _ = ctx.download_cross(st.base.shape[0], 6)
     ctx.intra_end()

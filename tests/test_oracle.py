@@ -500,3 +500,17 @@ def test_large_group_graph_reverse_rule(oracle):
     # nearest is 1; reverse lists: point r has source r+1 only, point 0 has source 1
     assert list(rows[0, :3]) == [1, 1, 0]  # forward 1 = reverse 1: one candidate
     assert list(rows[5, :4]) == [2, 4, 6, 5]
+
+
+@pytest.mark.parametrize("dim", [3, 8, 13, 128, 384, 768])
+def test_l2_pairs_matches_reference(oracle, ref_oracle, dim):
+    """The batched pair distance used by the full-size GPU checks equals the reference's
+    compiled FloatL2DistanceHandler pair by pair (and +inf on the padding id)."""
+    rng = np.random.default_rng(dim)
+    X = rng.standard_normal((300, dim)).astype(np.float32)
+    a = rng.integers(0, 300, 2000).astype(np.uint32)
+    b = rng.integers(0, 300, 2000).astype(np.uint32)
+    b[::11] = 0xFFFFFFFF
+    got = oracle.l2_pairs(X, a, b)
+    want = np.array([np.inf if y == 0xFFFFFFFF else ref_oracle.l2(X[x], X[y]) for x, y in zip(a, b)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
