@@ -16,13 +16,22 @@ collected after the additional edges (ung_hip_intra_end); --sequential runs the 
 one after the other.  Cross and intra results stay in HBM.  value = (P_cross +
 P_intra) / step time (distance evaluations/s, algorithmic pairs only).
 
+After the timed steps (not part of `value`):
+  * the drop-in calls with host output (ung_hip_cross_topk: FlatId rows, distances and
+    sizes copied to host memory; ung_hip_group_knn likewise) are timed, D2H included;
+  * the CPU baseline: the reference's own compiled distance + SearchQueue scan
+    (oracle/_ref) on a bounded random sample of cross-edge rows and of mid groups;
+  * parity of the same run: the GPU rows of those samples against the reference's rows.
+
 Prints ONE JSON line.
 """
 from __future__ import annotations
 
 import argparse
 import ctypes as C
+import hashlib
 import json
+import math
 import os
 import sys
 import time
@@ -36,27 +45,50 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense
 MFMA_FP32_PEAK_TFLOPS = 157.3
 HBM_PEAK_GBS = 8000.0
 METRIC = "cross-edge build wall time + distance evals/s (MFMA util %), 1M×128 fp32, 1 GPU"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_select_cross_cfg2.txt")
+TIE_BAND = 1e-5  # relative distance gap of BASELINE.json's tie band
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _sha256_files(paths, extra=b""):
+    h = hashlib.sha256()
+    for p in paths:
+        with open(p, "rb") as f:
+            h.update(f.read())
+    h.update(extra)
+    return h.hexdigest()
+
+
+def kernel_source_digest():
+    """Digest of what the device code is built from (ung_kernels.hip, which holds every
+    kernel, and the HIP compile flags): a traffic measurement holds while this is
+    unchanged.  Host-side files (ung_runtime.hip, ung_host.cpp) do not enter it."""
+    from filtervectorcode_refactor_amd import build as B
+    return _sha256_files([os.path.join(B.CSRC, "ung_kernels.hip")], " ".join(B.HIP_FLAGS).encode())
+
+
 def read_traffic(config_name):
-    """HBM bytes per launch of the cross select kernel on cfg2, measured offline with
-    rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and calibrated on a copy kernel; None for
-    other workloads (not measured)."""
-    if config_name != "cfg2" or not os.path.exists(TRAFFIC_FILE):
-        return None
-    with open(TRAFFIC_FILE) as f:
+    """HBM bytes per launch of the cross select kernel on this workload, measured offline
+    with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), calibrated on a copy kernel, from
+    profiles/traffic_select_cross_<config>.txt.  Returns (bytes or None, status): a file
+    whose kernel_source_sha256 differs from the current source is stale and not used."""
+    path = os.path.join(ROOT, "profiles", f"traffic_select_cross_{config_name}.txt")
+    if not os.path.exists(path):
+        return None, "not measured"
+    fields = {}
+    with open(path) as f:
         for line in f:
-            if line.startswith("traffic_bytes_per_launch:"):
-                try:
-                    return float(line.split(":", 1)[1].strip())
-                except ValueError:
-                    return None
-    return None
+            if ":" in line and line.split(":", 1)[0] in ("traffic_bytes_per_launch", "kernel_source_sha256"):
+                key, val = line.split(":", 1)
+                fields[key] = val.strip()
+    if fields.get("kernel_source_sha256") != kernel_source_digest():
+        return None, f"stale ({os.path.basename(path)} was measured on another kernel source)"
+    try:
+        return float(fields["traffic_bytes_per_launch"]), f"measured ({os.path.basename(path)})"
+    except (KeyError, ValueError):
+        return None, "unreadable"
 
 
 def calib_copy(nbytes):
@@ -76,60 +108,145 @@ def calib_copy(nbytes):
     log(f"calibration copy {nbytes} bytes done")
 
 
-def cpu_baseline(st, k, seconds=12.0, threads=None):
-    """The reference's own compiled distance + SearchQueue (oracle/_ref) when built,
-    else the plain-C oracle, on a bounded random sample of cross-edge queries."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _rows_parity(g_ids, g_dist, r_ids, r_dist):
+    """(rows, id-exact rows, distance-bit-exact rows) of GPU rows against reference rows."""
+    ids_ok = (g_ids == r_ids).all(axis=1)
+    dist_ok = (g_dist.view(np.uint32) == r_dist.view(np.uint32)).all(axis=1)
+    return int(g_ids.shape[0]), int(ids_ok.sum()), int(dist_ok.sum())
+
+
+def _tie_pairs(dist):
+    """Adjacent entries of sorted rows whose fp32 distances differ by at most TIE_BAND
+    relative (ties included); +inf padding ignored."""
+    d0, d1 = dist[:, :-1].astype(np.float64), dist[:, 1:].astype(np.float64)
+    ok = np.isfinite(d1)
+    return int(((d1 - d0 <= TIE_BAND * d1) & ok).sum())
+
+
+def cpu_leg_and_parity(st, cfg, gpu_cross, gpu_intra, p_cross, p_intra, seconds, timed=True):
+    """The reference's compiled scan (oracle/_ref; else the plain-C oracle) on a bounded
+    random sample of the workload -- cross-edge rows for about 2/3 of `seconds`, whole mid
+    groups for the rest -- timed on all host threads, and the GPU rows of the same
+    samples compared with its rows.  Returns (cpu_baseline or None, parity)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, RefOracle, ref_available
-    threads = threads or int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     kind = "reference" if ref_available() else "port"
-    lib = RefOracle() if kind == "reference" else Oracle()
+    ref = RefOracle() if kind == "reference" else Oracle()
+    k, K = cfg.k_cross, cfg.k_intra
     sizes = np.diff(st.group_begin.astype(np.int64))[1:]
-    out_cnt = np.diff(st.out_ptr.astype(np.int64))[1:]
+    cnt = np.diff(st.out_ptr.astype(np.int64))[1:]
     union = np.zeros(st.num_groups + 1, np.int64)
-    for c in np.nonzero(out_cnt)[0] + 1:
-        xs = st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]].astype(np.int64)
-        union[c] = int(sizes[xs - 1].sum())
-    point_group = st.new_vec_id_to_group_id
-    eligible = np.nonzero(union[point_group] > 0)[0].astype(np.uint32)
+    np.add.at(union, np.repeat(np.arange(1, st.num_groups + 1), cnt), sizes[st.out_idx.astype(np.int64) - 1])
+    pg = st.new_vec_id_to_group_id
+    eligible = np.nonzero(union[pg] > 0)[0].astype(np.uint32)
     rng = np.random.default_rng(7)
     rng.shuffle(eligible)
 
-    def run(nq):
-        q = eligible[:nq]
+    # cross leg: a calibration run, then one run sized to the budget; the reference scan
+    # keeps k+1 entries so the k-th / (k+1)-th boundary can be checked for the tie band
+    def cross_run(q):
         t0 = time.perf_counter()
-        if kind == "reference":
-            lib.cross_exact_points(st.base, st.group_begin, point_group, st.out_ptr, st.out_idx, q, k, threads)
-        else:
-            lib.cross_exact_points(st.base, st.group_begin, point_group, st.out_ptr, st.out_idx, q, k, threads)
-        dt = time.perf_counter() - t0
-        return int(union[point_group[q]].sum()), dt
+        ri, rd = ref.cross_exact_points(st.base, st.group_begin, pg, st.out_ptr, st.out_idx, q, k + 1, threads)
+        return ri, rd, time.perf_counter() - t0
 
-    nq = min(len(eligible), 64)
-    pairs, dt = run(nq)
-    while dt < seconds / 8 and nq < len(eligible):
-        nq = min(len(eligible), nq * 4)
-        pairs, dt = run(nq)
-    if dt < seconds / 2 and nq < len(eligible):
-        nq = min(len(eligible), int(nq * (seconds / max(dt, 1e-3))))
-        pairs, dt = run(nq)
-    return {"value": pairs / dt, "unit": "distance evals/s", "cores": threads, "kind": kind,
-            "sample": f"{nq} random cross-edge query points of cfg2 (exact scan of each point's "
-                      f"minimum-superset union, {pairs} pairs, {dt:.1f} s, {threads} OpenMP threads)"}
+    budget_x = seconds * 2 / 3 if timed else 0.0
+    q1 = eligible[: min(eligible.size, 256 if timed else 3000)]
+    ri, rd, dt1 = cross_run(q1)
+    qs, ris, rds = [q1], [ri], [rd]
+    pairs_x, dt_x = int(union[pg[q1]].sum()), dt1
+    if timed and q1.size < eligible.size and dt1 < budget_x:
+        rate = pairs_x / max(dt1, 1e-3)
+        cum = np.cumsum(union[pg[eligible[q1.size:]]])
+        n2 = int(np.searchsorted(cum, rate * (budget_x - dt1))) + 1
+        q2 = eligible[q1.size: q1.size + n2]
+        ri, rd, dt2 = cross_run(q2)
+        qs.append(q2)
+        ris.append(ri)
+        rds.append(rd)
+        pairs_x += int(union[pg[q2]].sum())
+        dt_x += dt2
+    q = np.concatenate(qs)
+    r_ids, r_dist = np.concatenate(ris), np.concatenate(rds)
+    g_ids, g_dist = gpu_cross
+    n_x, ok_x, okd_x = _rows_parity(g_ids[q], g_dist[q], r_ids[:, :k], r_dist[:, :k])
+    tie_x = _tie_pairs(r_dist)
+    d_k, d_k1 = r_dist[:, k - 1].astype(np.float64), r_dist[:, k].astype(np.float64)
+    boundary_x = int((np.isfinite(d_k1) & (d_k1 - d_k <= TIE_BAND * d_k1)).sum())
+
+    # intra leg: whole mid groups in random order until the rest of the budget is spent
+    gi_ids, gi_dist, gids, begins, gsz = gpu_intra
+    starts = np.cumsum(gsz.astype(np.int64)) - gsz.astype(np.int64)
+    order = rng.permutation(len(gids)) if len(gids) else np.zeros(0, np.int64)
+    budget_i = seconds - dt_x if timed else 0.0
+    pairs_i, dt_i, n_i, ok_i, okd_i, tie_i, groups_i = 0, 0.0, 0, 0, 0, 0, 0
+    for j in order:
+        b, n, r0 = int(begins[j]), int(gsz[j]), int(starts[j])
+        t0 = time.perf_counter()
+        oi, od = ref.intra_exact(st.base, b, n, K, threads)
+        dt_i += time.perf_counter() - t0
+        pairs_i += n * (n - 1)
+        a, b2, c = _rows_parity(gi_ids[r0: r0 + n], gi_dist[r0: r0 + n], oi, od)
+        n_i, ok_i, okd_i = n_i + a, ok_i + b2, okd_i + c
+        tie_i += _tie_pairs(od)
+        groups_i += 1
+        if dt_i >= budget_i and groups_i >= (1 if timed else 5):
+            break
+
+    parity = {
+        "cross_rows_checked": n_x, "cross_id_exact_rate": ok_x / max(n_x, 1),
+        "cross_dist_bitexact_rate": okd_x / max(n_x, 1),
+        "intra_rows_checked": n_i, "intra_groups_checked": groups_i, "intra_id_exact_rate": ok_i / max(n_i, 1),
+        "intra_dist_bitexact_rate": okd_i / max(n_i, 1),
+        "tie_band_pairs": tie_x + tie_i,
+        "tie_band_kth_boundary_rows": boundary_x,
+        "tie_band": f"adjacent entries of the reference's sorted rows (cross: top-{k + 1}, intra: top-{K}) within "
+                    f"{TIE_BAND:g} relative; kth_boundary = cross rows whose {k}-th and {k + 1}-th differ by at most that",
+        "checker": f"oracle/_ref ({kind}: the reference's compiled distance.cpp + search_queue.cpp scan)",
+    }
+    if not timed:
+        return None, parity
+    r_x = pairs_x / dt_x
+    r_i = pairs_i / dt_i if dt_i > 0 else None
+    if r_i and p_intra:
+        value = (p_cross + p_intra) / (p_cross / r_x + p_intra / r_i)  # the workload's mix
+    else:
+        value = r_x
+    base = {
+        "value": value, "unit": "distance evals/s", "cores": threads, "kind": kind, "cpu_model": cpu_model(),
+        "cross_evals_per_s": r_x, "intra_evals_per_s": r_i,
+        "sample": f"{q.size} random cross-edge rows of {cfg.name} (exact scan of each row's minimum-superset union, "
+                  f"{pairs_x} pairs, {dt_x:.1f} s) and {groups_i} random mid groups ({pairs_i} pairs, {dt_i:.1f} s), "
+                  f"{threads} OpenMP threads; value = the workload's P_cross + P_intra over the time those two rates "
+                  f"give for it",
+    }
+    return base, parity
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=0, help="timed steps (default: enough for about 2.5 s)")
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--n", type=int, default=0, help="override point count (smaller runs)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the timed CPU baseline (parity is still checked on a small sample)")
     ap.add_argument("--sequential", action="store_true",
                     help="cross edges, additional edges and the mid groups' kNN one after the other "
                          "(default: the kNN overlapped on the second stream)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="end with a 1 GiB device-to-device copy (counter calibration for --pmc runs)")
     args = ap.parse_args()
@@ -177,19 +294,36 @@ def main():
         s2 = ctx.group_knn_device(begins, sizes, cfg.k_intra) if args.sequential else ctx.intra_end()
         return s1, s2, s3
 
-    for _ in range(args.warmup):
+    warmup = max(args.warmup, 1 if args.steps <= 0 else 0)
+    per = None
+    for _ in range(warmup):
+        t_w = time.perf_counter()
         step()
-    ctx.synchronize()
+        ctx.synchronize()
+        per = time.perf_counter() - t_w  # the last warmup step (the first one allocates)
+    steps = args.steps
+    if steps <= 0:  # enough timed steps for about 2.5 s at the last warmup step's pace
+        steps = max(3, int(math.ceil(2.5 / max(per, 1e-4))))
     cross_stats, intra_stats, addl_stats = [], [], []
+    ctx.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         s1, s2, s3 = step()
         cross_stats.append(s1)
         intra_stats.append(s2)
         addl_stats.append(s3)
     ctx.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
+    ms_per_step = wall * 1e3 / steps
+    log(f"{steps} timed steps: {ms_per_step:.3f} ms/step")
+
+    # the drop-in calls with host output (D2H included), after the timed region
+    dropin = [ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross) for _ in range(3)]
+    g_cross = (dropin[-1][0], dropin[-1][1])
+    cross_rescanned = int(dropin[-1][3]["fallback_rows"])
+    intra_dropin = [ctx.group_knn(begins, sizes, cfg.k_intra) for _ in range(2)]
+    g_intra = (intra_dropin[-1][0], intra_dropin[-1][1], gids, begins, sizes)
+    intra_rescanned = int(intra_dropin[-1][2]["fallback_rows"])
 
     def avg(lst, key):
         return float(np.mean([s[key] for s in lst]))
@@ -200,29 +334,30 @@ def main():
     dp = (d + 31) // 32 * 32
     # The cross select kernel's two floors: its MFMA work (three bf16 products per fp32
     # product: 3 * 2 * dp flops per algorithmic pair, against the dense bf16 peak) and its
-    # HBM traffic (measured, against 8 TB/s).  The larger floor is the roofline that
-    # bounds it; achieved = algorithmic bytes (query + candidate rows each work item
-    # streams) or flops per launch / the launch's average duration.
+    # HBM traffic (measured with rocprofv3 on this kernel source, against 8 TB/s).  The
+    # larger floor bounds it; without a valid traffic measurement the MFMA floor is used.
     sel_s = sel_cross_ms * 1e-3
     flops_cross = 2.0 * d * p_cross
     mfma_flops = 3.0 * 2.0 * dp * p_cross
     alg_bytes = float(cross_stats[-1]["select_bytes"])
-    traffic = read_traffic(cfg.name) if not args.n else None
+    traffic, traffic_status = read_traffic(cfg.name) if not args.n else (None, "not measured (scaled run)")
     mfma_floor_ms = mfma_flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e3
-    hbm_floor_ms = (traffic if traffic else alg_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3
+    hbm_floor_ms = traffic / (HBM_PEAK_GBS * 1e9) * 1e3 if traffic else None
     mfma_tflops = mfma_flops / sel_s / 1e12
-    hbm_gbs = alg_bytes / sel_s / 1e9
-    if hbm_floor_ms >= mfma_floor_ms:
-        roofline = {"bound": "hbm", "achieved": round(hbm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(hbm_gbs / HBM_PEAK_GBS, 4), "traffic": traffic}
+    if hbm_floor_ms is not None and hbm_floor_ms >= mfma_floor_ms:
+        ach = traffic / sel_s / 1e9
+        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic}
     else:
         roofline = {"bound": "mfma", "achieved": round(mfma_tflops, 3), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(mfma_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic}
     roofline.update({
-        "kernel": ("ung_select_kernel<8,1,false,2,true> (cross edges, register-query layout, one launch per step)"
-                   if dp == 128 else "ung_select_kernel<8,1,false,2,false> (cross edges, one launch per step)"),
+        "kernel": ("ung_select_kernel<8,*,false,2,true> (cross edges, register-query layout, one launch per step)"
+                   if dp == 128 else "ung_select_kernel<8,*,false,2,false> (cross edges, one launch per step)"),
         "avg_launch_ms": round(sel_cross_ms, 4),
-        "alg_bytes_per_launch": alg_bytes, "hbm_floor_ms": round(hbm_floor_ms, 3),
+        "traffic_status": traffic_status,
+        "streamed_operand_bytes_per_launch": alg_bytes,
+        "hbm_floor_ms": round(hbm_floor_ms, 3) if hbm_floor_ms is not None else None,
         "mfma_bf16_flops_per_launch": mfma_flops, "mfma_floor_ms": round(mfma_floor_ms, 3),
         "mfma_bf16_tflops": round(mfma_tflops, 2), "mfma_bf16_frac": round(mfma_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         "measured_hbm_gbs": round(traffic / sel_s / 1e9, 1) if traffic else None,
@@ -231,8 +366,9 @@ def main():
     value = (p_cross + p_intra) / (ms_per_step * 1e-3)
     result = {
         "metric": METRIC, "value": value, "unit": "distance evals/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32 (3xbf16 MFMA pre-select, exact f32 re-score)",
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (3xbf16 MFMA pre-select, exact f32 re-score)",
         "data": "synthetic",
         "config": {"workload": f"{cfg.name}: {cfg.n}x{cfg.dim} fp32 Gaussian mixture "
                                f"({cfg.n_centroids} centroids, sigma {cfg.sigma}), vocab {cfg.vocab}, "
@@ -262,11 +398,23 @@ def main():
             "intra_select_tflops": round(2.0 * d * p_intra / (sel_intra_ms * 1e-3) / 1e12, 3) if p_intra else None,
             "cross_evals_per_s": p_cross / (avg(cross_stats, "wall_ms") * 1e-3),
             "resident_upload_ms": round(up["h2d_ms"], 3),
+            "cross_dropin_wall_ms": round(float(np.mean([s[3]["wall_ms"] for s in dropin])), 3),
+            "cross_dropin_d2h_ms": round(float(np.mean([s[3]["d2h_ms"] for s in dropin])), 3),
+            "intra_dropin_wall_ms": round(float(np.mean([s[2]["wall_ms"] for s in intra_dropin])), 3),
+            "intra_dropin_d2h_ms": round(float(np.mean([s[2]["d2h_ms"] for s in intra_dropin])), 3),
+            "dropin_note": "ung_hip_cross_topk / ung_hip_group_knn with host output (FlatId rows + distances + "
+                           "sizes, D2H included), run after the timed steps; the one-time upload of X is "
+                           "resident_upload_ms",
         },
     }
-    if not args.no_cpu_baseline:
-        log("cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(st, cfg.k_cross, seconds=args.cpu_seconds)
+    log("cpu baseline + parity ..." if not args.no_cpu_baseline else "parity ...")
+    base, parity = cpu_leg_and_parity(st, cfg, g_cross, g_intra, p_cross, p_intra, args.cpu_seconds,
+                                      timed=not args.no_cpu_baseline)
+    parity["cross_rescanned_rows"] = cross_rescanned
+    parity["intra_rescanned_rows"] = intra_rescanned
+    result["parity"] = parity
+    if base is not None:
+        result["cpu_baseline"] = base
     st.close()
     if args.calib_copy:
         calib_copy(1 << 30)

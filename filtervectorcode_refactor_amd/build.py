@@ -3,7 +3,8 @@
 The library is built in-tree (filtervectorcode_refactor_amd/libung_hip.so) so it
 travels with the repository snapshot to the GPU box:
   * ung_host.cpp    -> g++ (host C++: synthetic inputs, groups, LNG, reorder)
-  * ung_kernels.hip -> hipcc --offload-arch=gfx950 (kernels + device C ABI)
+  * ung_runtime.hip -> hipcc --offload-arch=gfx950 (context, planning, launches, C ABI;
+                       includes ung_kernels.hip, the device code: one translation unit)
 Packed-FP32 instruction selection is disabled for all device code.
 """
 from __future__ import annotations
@@ -51,9 +52,9 @@ def build(verbose: bool = True) -> str:
     host_obj = os.path.join(obj_dir, "ung_host.o")
     _run([CXX, *HOST_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
           os.path.join(CSRC, "ung_host.cpp"), "-o", host_obj], verbose)
-    dev_obj = os.path.join(obj_dir, "ung_kernels.o")
+    dev_obj = os.path.join(obj_dir, "ung_runtime.o")
     _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
-          os.path.join(CSRC, "ung_kernels.hip"), "-o", dev_obj], verbose)
+          os.path.join(CSRC, "ung_runtime.hip"), "-o", dev_obj], verbose)
     tmp = LIB_PATH + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", dev_obj, host_obj,
           "-o", tmp, "-pthread"], verbose)

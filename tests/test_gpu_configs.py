@@ -13,7 +13,8 @@
   - every row the certificate sent to the exact rescan, plus a large random sample of
     rows, bit-exact against the reference's compiled distance + SearchQueue scan
     (oracle/_ref, else the plain-C oracle);
-  - the additional edges of a sample of groups against the oracle fed the GPU's cross rows;
+  - the additional edges of every group (a random sample when the oracle's scan would
+    exceed its budget) against the oracle fed the GPU's cross rows;
   - every intra row (mid groups, K = 32): size, local ids, no self, (dist, id) order,
     distances bit-exact; every rescanned intra row and a sample of groups bit-exact.
 """
@@ -145,7 +146,7 @@ def _full_size(cfg_name, oracle, n_cross_sample, n_intra_groups, addl_budget_dim
     res = chk.cross_exact_points(st.base, st.group_begin, pg, st.out_ptr, st.out_idx, q, k)
     _assert_rows_equal(ids[q], dist[q], None, res[0], res[1], None, f"{cfg_name} full cross rows")
 
-    # additional edges of a sample of groups (each group's list depends only on its own
+    # additional edges of every group, or a sample within the budget (each group's list depends only on its own
     # cross rows and LNG row, so the oracle gets an LNG with only those rows)
     ep, ef, et, ast = ctx.additional_edges(st.group_begin, st.out_ptr, st.out_idx, k)
     _say(f"{cfg_name} full: {ef.size} additional edges, {ast['rows']} query rows")
@@ -156,23 +157,23 @@ def _full_size(cfg_name, oracle, n_cross_sample, n_intra_groups, addl_budget_dim
         grp = np.repeat(np.arange(G + 2), np.diff(np.concatenate([ep.astype(np.int64), [ep[-1]]])))[: et.size]
         np.add.at(cost, grp, xs * cfg.dim / np.minimum(xs, k // 2))
     has_out = np.nonzero(cnt > 0)[0] + 1
-    order = rng.permutation(has_out)
-    pick, spent = [], 0.0
-    for c in order:
-        if spent + cost[c] > addl_budget_dims:
-            continue
-        pick.append(int(c))
-        spent += cost[c]
-        if len(pick) >= 4000:
-            break
-    pick = np.sort(np.array(pick, np.int64))
+    if cost[has_out].sum() <= addl_budget_dims:  # every group
+        pick, spent = has_out.astype(np.int64), float(cost[has_out].sum())
+    else:  # a random sample within the budget
+        pick, spent = [], 0.0
+        for c in rng.permutation(has_out):
+            if spent + cost[c] <= addl_budget_dims:
+                pick.append(int(c))
+                spent += cost[c]
+        pick = np.sort(np.array(pick, np.int64))
     keep = np.zeros(G + 1, bool)
     keep[pick] = True
     rcnt = cnt * keep[1:]
     rop = np.zeros(G + 2, np.uint32)
     rop[2:] = np.cumsum(rcnt)
     roi = np.concatenate([st.out_idx[st.out_ptr[c]: st.out_ptr[c + 1]] for c in pick]).astype(np.uint32)
-    _say(f"{cfg_name} full: additional edges of {pick.size} groups against the oracle ({spent:.2e} dims)")
+    _say(f"{cfg_name} full: additional edges of {pick.size} of {has_out.size} groups with out-groups against the "
+         f"oracle ({spent:.2e} dims)")
     wp, wf, wt = oracle.additional_edges(st.base, st.group_begin, rop, roi, ids, k)
     n_with = 0
     for c in pick:
