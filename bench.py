@@ -131,7 +131,8 @@ def _tie_pairs(dist):
     relative (ties included); +inf padding ignored."""
     d0, d1 = dist[:, :-1].astype(np.float64), dist[:, 1:].astype(np.float64)
     ok = np.isfinite(d1)
-    return int(((d1 - d0 <= TIE_BAND * d1) & ok).sum())
+    with np.errstate(invalid="ignore"):
+        return int(((d1 - d0 <= TIE_BAND * d1) & ok).sum())
 
 
 def cpu_leg_and_parity(st, cfg, gpu_cross, gpu_intra, p_cross, p_intra, seconds, timed=True):
@@ -183,7 +184,8 @@ def cpu_leg_and_parity(st, cfg, gpu_cross, gpu_intra, p_cross, p_intra, seconds,
     n_x, ok_x, okd_x = _rows_parity(g_ids[q], g_dist[q], r_ids[:, :k], r_dist[:, :k])
     tie_x = _tie_pairs(r_dist)
     d_k, d_k1 = r_dist[:, k - 1].astype(np.float64), r_dist[:, k].astype(np.float64)
-    boundary_x = int((np.isfinite(d_k1) & (d_k1 - d_k <= TIE_BAND * d_k1)).sum())
+    with np.errstate(invalid="ignore"):
+        boundary_x = int((np.isfinite(d_k1) & (d_k1 - d_k <= TIE_BAND * d_k1)).sum())
 
     # intra leg: whole mid groups in random order until the rest of the budget is spent
     gi_ids, gi_dist, gids, begins, gsz = gpu_intra
