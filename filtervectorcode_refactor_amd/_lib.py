@@ -69,6 +69,7 @@ SIGNATURES = {
     "ung_hip_cross_topk": (_int, [_vp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     "ung_hip_cross_topk_device": (_int, [_vp, _u32, _vp, _vp, _vp, _u32, _vp]),
     "ung_hip_cross_result_device": (_int, [_vp, _vp, _vp]),
+    "ung_hip_cross_topk_noalloc": (_int, [_vp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     "ung_hip_download_cross": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "ung_hip_additional_edges": (_int, [_vp, _u32, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _u64, C.POINTER(_u64), _vp]),
     "ung_hip_group_knn": (_int, [_vp, _u32, _vp, _vp, _u32, _vp, _vp, _vp]),

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "ung_hip.h"
@@ -134,6 +135,55 @@ struct ResultBufs {
 } // namespace
 
 namespace {
+// Host staging of a plan's uploads: jobs | items (sorted) | seg_start | seg_vend | merge
+// items (written after the select kernel is enqueued, so building and uploading them
+// overlaps it); 256-byte aligned parts.
+struct StageLayout {
+    size_t bj, bi, bs, bm;     // bytes of jobs, items, each segment array, merge items
+    size_t oj, oi, os, ov, om; // offsets
+    size_t total;
+};
+
+StageLayout stage_layout(const Plan &pl)
+{
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    StageLayout L{};
+    L.bj = pl.jobs.size() * sizeof(Job);
+    L.bi = pl.items.size() * sizeof(Item);
+    L.bs = pl.seg_start.size() * sizeof(uint32_t);
+    L.bm = pl.n_mitems * sizeof(MergeItem);
+    L.oj = 0;
+    L.oi = al(L.bj);
+    L.os = L.oi + al(L.bi);
+    L.ov = L.os + al(L.bs);
+    L.om = L.ov + al(L.bs);
+    L.total = L.om + al(L.bm);
+    return L;
+}
+
+// Where a planned call reads its work lists, keeps its partial rows and flags, and
+// writes its result rows.
+struct PlanMem {
+    Job *jobs = nullptr;
+    Item *items = nullptr;
+    MergeItem *mitems = nullptr;
+    uint32_t *seg_start = nullptr, *seg_vend = nullptr;
+    uint32_t *part_ids = nullptr;
+    float *part_dist = nullptr, *part_bound = nullptr;
+    uint32_t *flag_count = nullptr; // [0]: rows flagged for the rescan, [1]: select item counter
+    uint2 *flagged = nullptr;
+    uint32_t *out_ids = nullptr;    // result rows
+    float *out_dist = nullptr;
+    int32_t *out_size = nullptr;
+    std::vector<uint32_t> *rescanned = nullptr; // output rows that took the exact rescan
+    char *stage = nullptr;          // host staging (stage_layout), stable until the call ends
+    // rescan range partials: grown in the workspace on demand, or a fixed region
+    bool fb_grow = true;
+    uint32_t *fb_ids = nullptr;
+    float *fb_dist = nullptr;
+    uint64_t fb_cap = 0;            // entries of fb_ids / fb_dist when !fb_grow
+};
+
 // Work lists, partial rows, flags and timing events of one planned call, with the stream
 // it runs on.  A context has two, so a group kNN call can run on the second stream while
 // the cross-edge call and the additional edges use the first.
@@ -195,6 +245,12 @@ struct ung_hip_ctx {
     // storage is reused instead of allocated and first touched again every call
     Plan plan0;
     Plan intra_plan;
+    PlanMem intra_mem; // memory of the group call in flight on ws[1]
+    // ung_hip_cross_topk_noalloc: this device's address of the file-scope scratch array
+    // (resolved once per device at ung_hip_create), host staging and rescanned rows
+    unsigned char *scratch_dev = nullptr;
+    std::vector<char> noalloc_stage;
+    std::vector<uint32_t> noalloc_rescanned;
     uint32_t intra_list_k = 0;
     ung_hip_stats intra_stats{};
     std::chrono::steady_clock::time_point intra_t0;
@@ -393,17 +449,11 @@ double eps_coef_for(uint32_t d)
     return (1.75 * (double)d + 112.0) * std::ldexp(1.0, -24);
 }
 
-// Runs a planned job list on workspace `ws`; results into `res` (rows x k), rows of res
-// already initialised by the caller when some rows have no job.  plan_launch uploads the
-// work lists and enqueues the select and merge kernels; plan_finish reads the flagged-row
-// count back, rescans those rows and collects the statistics.
-int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st,
-                hipEvent_t start_after = nullptr)
+// PlanMem in the workspace's own buffers, grown to the plan (hipMalloc / hipHostMalloc
+// when a buffer is too small); rows into `res`.
+int workspace_mem(Workspace &ws, const Plan &pl, uint32_t lp, ResultBufs &res, PlanMem &m)
 {
     int rc;
-    const int lt = pick_lt(k);
-    const uint32_t lp = pick_lp(k, lt);
-    const auto t_h2d = clk::now();
     if ((rc = ws.jobs.ensure(pl.jobs.size())) || (rc = ws.items.ensure(pl.items.size())) ||
         (rc = ws.mitems.ensure(pl.n_mitems)) || (rc = ws.seg_start.ensure(pl.seg_start.size())) ||
         (rc = ws.seg_vend.ensure(pl.seg_vend.size())) ||
@@ -411,26 +461,52 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
         (rc = ws.part_bound.ensure(pl.part_rows)) || (rc = ws.flag_count.ensure(2)) ||
         (rc = ws.flagged.ensure(std::max<uint64_t>(pl.rows, 1))))
         return rc;
-    // select items in order of decreasing cost (candidate tiles); the stable sort keeps
-    // the query blocks of one split next to each other
-    // (a counting sort by tile count: stable, linear in the item count)
-    // staging layout: jobs | items | seg_start | seg_vend | merge items (written after the
-    // select kernel is enqueued, so building and uploading them overlaps it)
-    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    const size_t bj = pl.jobs.size() * sizeof(Job), bi = pl.items.size() * sizeof(Item);
-    const size_t bm = pl.n_mitems * sizeof(MergeItem), bs = pl.seg_start.size() * sizeof(uint32_t);
-    const size_t oj = 0, oi = al(bj), os = oi + al(bi), ov = os + al(bs), om = ov + al(bs);
-    char *hs = nullptr;
     if (!pl.jobs.empty()) {
-        // the previous call's uploads from this staging buffer have completed (its merge
+        // the previous call's uploads from the staging buffer have completed (its merge
         // launch event follows them on the stream)
         HIPCHECK(hipEventSynchronize(ws.ev[2]));
-        if ((rc = ws.stage.ensure(om + al(bm))))
+        if ((rc = ws.stage.ensure(stage_layout(pl).total)))
             return rc;
-        hs = static_cast<char *>(ws.stage.p);
-        std::memcpy(hs + oj, pl.jobs.data(), bj);
-        std::memcpy(hs + os, pl.seg_start.data(), bs);
-        std::memcpy(hs + ov, pl.seg_vend.data(), bs);
+    }
+    m.jobs = ws.jobs.p;
+    m.items = ws.items.p;
+    m.mitems = ws.mitems.p;
+    m.seg_start = ws.seg_start.p;
+    m.seg_vend = ws.seg_vend.p;
+    m.part_ids = ws.part_ids.p;
+    m.part_dist = ws.part_dist.p;
+    m.part_bound = ws.part_bound.p;
+    m.flag_count = ws.flag_count.p;
+    m.flagged = ws.flagged.p;
+    m.out_ids = res.ids.p;
+    m.out_dist = res.dist.p;
+    m.out_size = res.size.p;
+    m.rescanned = &res.rescanned;
+    m.stage = static_cast<char *>(ws.stage.p);
+    m.fb_grow = true;
+    return UNG_HIP_OK;
+}
+
+// Runs a planned job list on workspace `ws` (its stream and events) with the memory of
+// `m`; result rows already initialised by the caller when some rows have no job.
+// plan_launch uploads the work lists and enqueues the select and merge kernels;
+// plan_finish reads the flagged-row count back, rescans those rows and collects the
+// statistics.
+int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, PlanMem &m, ung_hip_stats *st,
+                hipEvent_t start_after = nullptr)
+{
+    int rc;
+    const int lt = pick_lt(k);
+    const uint32_t lp = pick_lp(k, lt);
+    const auto t_h2d = clk::now();
+    const StageLayout L = stage_layout(pl);
+    char *hs = m.stage;
+    if (!pl.jobs.empty()) {
+        std::memcpy(hs + L.oj, pl.jobs.data(), L.bj);
+        std::memcpy(hs + L.os, pl.seg_start.data(), L.bs);
+        std::memcpy(hs + L.ov, pl.seg_vend.data(), L.bs);
+        // select items in order of decreasing cost (candidate tiles): a counting sort by
+        // tile count, stable (the query blocks of one split stay next to each other)
         uint32_t max_t = 0;
         for (const Item &it : pl.items)
             max_t = std::max(max_t, (it.v_end - it.v_begin + BC - 1) / BC);
@@ -439,13 +515,13 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
             ++start[max_t - (it.v_end - it.v_begin + BC - 1) / BC + 1];
         for (uint32_t t = 0; t <= max_t; ++t)
             start[t + 1] += start[t];
-        Item *sorted = reinterpret_cast<Item *>(hs + oi);
+        Item *sorted = reinterpret_cast<Item *>(hs + L.oi);
         for (const Item &it : pl.items)
             sorted[start[max_t - (it.v_end - it.v_begin + BC - 1) / BC]++] = it;
-        HIPCHECK(hipMemcpyAsync(ws.jobs.p, hs + oj, bj, hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.items.p, hs + oi, bi, hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.seg_start.p, hs + os, bs, hipMemcpyHostToDevice, ws.stream));
-        HIPCHECK(hipMemcpyAsync(ws.seg_vend.p, hs + ov, bs, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(m.jobs, hs + L.oj, L.bj, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(m.items, hs + L.oi, L.bi, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(m.seg_start, hs + L.os, L.bs, hipMemcpyHostToDevice, ws.stream));
+        HIPCHECK(hipMemcpyAsync(m.seg_vend, hs + L.ov, L.bs, hipMemcpyHostToDevice, ws.stream));
     }
     if (st)
         st->h2d_ms += ms_since(t_h2d);
@@ -455,8 +531,7 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     // kernels of this plan start after `start_after` (another stream's event), if given
     if (start_after)
         HIPCHECK(hipStreamWaitEvent(ws.stream, start_after, 0));
-    // flag_count[0]: rows flagged for the fallback, [1]: select item counter
-    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ws.stream, ws.flag_count.p, 2u);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ws.stream, m.flag_count, 2u);
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipEventRecord(ws.ev[0], ws.stream));
 
@@ -465,17 +540,17 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     P.xn = ctx->xn;
     P.dp = ctx->dp;
     P.k = k;
-    P.jobs = ws.jobs.p;
-    P.items = ws.items.p;
-    P.seg_start = ws.seg_start.p;
-    P.seg_vend = ws.seg_vend.p;
-    P.part_ids = ws.part_ids.p;
-    P.part_dist = ws.part_dist.p;
-    P.part_bound = ws.part_bound.p;
+    P.jobs = m.jobs;
+    P.items = m.items;
+    P.seg_start = m.seg_start;
+    P.seg_vend = m.seg_vend;
+    P.part_ids = m.part_ids;
+    P.part_dist = m.part_dist;
+    P.part_bound = m.part_bound;
     P.eps_coef = eps_coef_for(ctx->d) * ctx->eps_scale;
     P.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
     P.rmax = ctx->rmax;
-    P.item_ctr = ws.flag_count.p + 1;
+    P.item_ctr = m.flag_count + 1;
     P.lp = lp;
     const uint32_t n_items = (uint32_t)pl.items.size();
     const bool excl = (pl.jobs[0].flags & 1u) != 0; // one kind of job per plan
@@ -491,8 +566,8 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
 
     // merge items, built and uploaded (on the upload stream) while the select kernel runs
     const auto t_mi = clk::now();
-    write_merge_items(pl, reinterpret_cast<MergeItem *>(hs + om));
-    HIPCHECK(hipMemcpyAsync(ws.mitems.p, hs + om, bm, hipMemcpyHostToDevice, ws.upload));
+    write_merge_items(pl, reinterpret_cast<MergeItem *>(hs + L.om));
+    HIPCHECK(hipMemcpyAsync(m.mitems, hs + L.om, L.bm, hipMemcpyHostToDevice, ws.upload));
     HIPCHECK(hipEventRecord(ws.ev_up, ws.upload));
     HIPCHECK(hipStreamWaitEvent(ws.stream, ws.ev_up, 0));
     if (st)
@@ -502,21 +577,21 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     M.X = ctx->X;
     M.xn = ctx->xn;
     M.d = ctx->d;
-    M.jobs = ws.jobs.p;
-    M.mitems = ws.mitems.p;
-    M.part_ids = ws.part_ids.p;
-    M.part_dist = ws.part_dist.p;
-    M.part_bound = ws.part_bound.p;
+    M.jobs = m.jobs;
+    M.mitems = m.mitems;
+    M.part_ids = m.part_ids;
+    M.part_dist = m.part_dist;
+    M.part_bound = m.part_bound;
     M.lp = lp;
     M.k = k;
     M.eps_coef = P.eps_coef;
     M.shrink = P.shrink;
     M.rmax = P.rmax;
-    M.out_ids = res.ids.p;
-    M.out_dist = res.dist.p;
-    M.out_size = res.size.p;
-    M.flag_count = ws.flag_count.p;
-    M.flagged = ws.flagged.p;
+    M.out_ids = m.out_ids;
+    M.out_dist = m.out_dist;
+    M.out_size = m.out_size;
+    M.flag_count = m.flag_count;
+    M.flagged = m.flagged;
     const uint32_t n_m = (uint32_t)pl.n_mitems;
     for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
         MergeParams Mc = M;
@@ -529,39 +604,46 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     return UNG_HIP_OK;
 }
 
-int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st)
+int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, PlanMem &m, ung_hip_stats *st)
 {
     int rc;
     if (pl.jobs.empty())
         return UNG_HIP_OK;
     uint32_t nflag = 0;
-    HIPCHECK(hipMemcpyAsync(&nflag, ws.flag_count.p, sizeof(uint32_t), hipMemcpyDeviceToHost, ws.stream));
+    HIPCHECK(hipMemcpyAsync(&nflag, m.flag_count, sizeof(uint32_t), hipMemcpyDeviceToHost, ws.stream));
     HIPCHECK(hipStreamSynchronize(ws.stream));
     if (nflag > 0) {
         // a flagged row's union is cut into ranges of >= FALLBACK_RANGE candidates
         uint64_t max_cand = 0;
         for (const Job &jb : pl.jobs)
             max_cand = std::max<uint64_t>(max_cand, jb.n_cand);
-        const uint32_t S =
+        uint32_t S =
             (uint32_t)std::min<uint64_t>(MAX_FALLBACK_SPLITS, std::max<uint64_t>(1, max_cand / FALLBACK_RANGE));
+        if (!m.fb_grow) // the fixed region bounds the ranges (one range writes the row itself)
+            S = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(S, m.fb_cap / ((uint64_t)nflag * k)));
         FallbackParams F{};
         F.X = ctx->X;
         F.d = ctx->d;
         F.k = k;
-        F.jobs = ws.jobs.p;
-        F.seg_start = ws.seg_start.p;
-        F.seg_vend = ws.seg_vend.p;
-        F.flag_count = ws.flag_count.p;
-        F.flagged = ws.flagged.p;
+        F.jobs = m.jobs;
+        F.seg_start = m.seg_start;
+        F.seg_vend = m.seg_vend;
+        F.flag_count = m.flag_count;
+        F.flagged = m.flagged;
         F.splits = S;
-        F.out_ids = res.ids.p;
-        F.out_dist = res.dist.p;
-        F.out_size = res.size.p;
+        F.out_ids = m.out_ids;
+        F.out_dist = m.out_dist;
+        F.out_size = m.out_size;
         if (S > 1) {
-            if ((rc = ws.fb_ids.ensure((uint64_t)nflag * S * k)) || (rc = ws.fb_dist.ensure((uint64_t)nflag * S * k)))
-                return rc;
-            F.part_ids = ws.fb_ids.p;
-            F.part_dist = ws.fb_dist.p;
+            if (m.fb_grow) {
+                if ((rc = ws.fb_ids.ensure((uint64_t)nflag * S * k)) ||
+                    (rc = ws.fb_dist.ensure((uint64_t)nflag * S * k)))
+                    return rc;
+                m.fb_ids = ws.fb_ids.p;
+                m.fb_dist = ws.fb_dist.p;
+            }
+            F.part_ids = m.fb_ids;
+            F.part_dist = m.fb_dist;
         }
         const uint64_t items = (uint64_t)nflag * S;
         hipLaunchKernelGGL(ung_fallback_kernel, dim3((unsigned)std::min<uint64_t>(items, 1u << 20)), dim3(64), 0,
@@ -575,13 +657,15 @@ int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     }
     std::vector<uint2> flagged_host(nflag);
     if (nflag > 0)
-        HIPCHECK(hipMemcpyAsync(flagged_host.data(), ws.flagged.p, nflag * sizeof(uint2), hipMemcpyDeviceToHost,
+        HIPCHECK(hipMemcpyAsync(flagged_host.data(), m.flagged, nflag * sizeof(uint2), hipMemcpyDeviceToHost,
                                 ws.stream));
     HIPCHECK(hipEventRecord(ws.ev[3], ws.stream));
     HIPCHECK(hipEventSynchronize(ws.ev[3]));
-    for (const uint2 &f : flagged_host)
-        res.rescanned.push_back(pl.jobs[f.x].out_row + f.y);
-    std::sort(res.rescanned.begin(), res.rescanned.end());
+    if (m.rescanned) {
+        for (const uint2 &f : flagged_host)
+            m.rescanned->push_back(pl.jobs[f.x].out_row + f.y);
+        std::sort(m.rescanned->begin(), m.rescanned->end());
+    }
     if (st) {
         float a = 0, b = 0, c = 0;
         HIPCHECK(hipEventElapsedTime(&a, ws.ev[0], ws.ev[1]));
@@ -605,12 +689,14 @@ int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Res
     return UNG_HIP_OK;
 }
 
+// Launch + finish in the workspace's own (growable) memory, rows into `res`.
 int run_plan(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, ResultBufs &res, ung_hip_stats *st)
 {
     int rc;
-    if ((rc = plan_launch(ctx, ws, pl, k, res, st)))
+    PlanMem m;
+    if ((rc = workspace_mem(ws, pl, pick_lp(k, pick_lt(k)), res, m)) || (rc = plan_launch(ctx, ws, pl, k, m, st)))
         return rc;
-    return plan_finish(ctx, ws, pl, k, res, st);
+    return plan_finish(ctx, ws, pl, k, m, st);
 }
 
 int check_ready(ung_hip_ctx *ctx)
@@ -804,9 +890,14 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     ctx->intra_stats.plan_ms += ms_since(ctx->intra_t0);
     // the group call's kernels start when the cross select ends: they fill the chip while
     // the cross merge (memory-bound), rescan and the caller's next steps run
-    if ((rc = cross_prepare_result(ctx, k)) || (rc = plan_launch(ctx, ctx->ws[0], pl, k, ctx->cross, st)) ||
+    PlanMem m0;
+    if ((rc = cross_prepare_result(ctx, k)) ||
+        (rc = workspace_mem(ctx->ws[0], pl, pick_lp(k, pick_lt(k)), ctx->cross, m0)) ||
+        (rc = plan_launch(ctx, ctx->ws[0], pl, k, m0, st)) ||
         (rc = group_prepare_result(ctx, ctx->intra_plan, list_k)) ||
-        (rc = plan_launch(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats,
+        (rc = workspace_mem(ctx->ws[1], ctx->intra_plan, pick_lp(list_k, pick_lt(list_k)), ctx->group,
+                            ctx->intra_mem)) ||
+        (rc = plan_launch(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->intra_mem, &ctx->intra_stats,
                           ctx->ws[0].ev[1]))) {
         drain_after_failure(ctx);
         return rc;
@@ -814,7 +905,7 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     // from here the group call is in flight on the second workspace until intra_end
     ctx->intra_list_k = list_k;
     ctx->intra_pending = true;
-    rc = plan_finish(ctx, ctx->ws[0], pl, k, ctx->cross, st);
+    rc = plan_finish(ctx, ctx->ws[0], pl, k, m0, st);
     if (rc == UNG_HIP_OK && hipStreamSynchronize(ctx->ws[0].stream) != hipSuccess) {
         set_error("ung_hip_cross_intra_begin: stream synchronisation failed");
         rc = UNG_HIP_EDEVICE;
@@ -841,7 +932,7 @@ int intra_end(ung_hip_ctx *ctx, ung_hip_stats *st)
         return rc;
     ctx->intra_pending = false;
     const uint32_t list_k = ctx->intra_list_k;
-    if ((rc = plan_finish(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->group, &ctx->intra_stats)) ||
+    if ((rc = plan_finish(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->intra_mem, &ctx->intra_stats)) ||
         (rc = group_complete(ctx, ctx->ws[1], ctx->intra_plan, list_k))) {
         drain_after_failure(ctx);
         return rc;
@@ -1232,6 +1323,158 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Scratch of ung_hip_cross_topk_noalloc: one file-scope device array per GPU, held until
+// the process ends.  In host code `scratch` only names the symbol: kernels get the
+// device address resolved by hipGetSymbolAddress (per device, at ung_hip_create).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[UNG_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_SCRATCH_DEVICES = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_addr[MAX_SCRATCH_DEVICES] = {};
+
+// The device address of `scratch` on `device` (current), resolved once per device.
+int resolve_scratch(int device, unsigned char **addr)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= MAX_SCRATCH_DEVICES) {
+        set_error("no scratch address table entry for device %d", device);
+        return UNG_HIP_EINVAL;
+    }
+    if (!g_scratch_addr[device]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", device, hipGetErrorString(e));
+            return UNG_HIP_EDEVICE;
+        }
+        g_scratch_addr[device] = static_cast<unsigned char *>(ptr);
+    }
+    *addr = g_scratch_addr[device];
+    return UNG_HIP_OK;
+}
+
+// Carves a planned cross call's memory out of the scratch array: work lists, partial rows
+// and flags first, the rest for the rescan's range partials.  UNG_HIP_EINVAL when the plan
+// does not fit.
+int scratch_mem(ung_hip_ctx *ctx, const Plan &pl, uint32_t lp, PlanMem &m)
+{
+    auto al = [](uint64_t b) { return (b + 255) & ~(uint64_t)255; };
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        const uint64_t at = off;
+        off += al(bytes);
+        return at;
+    };
+    const uint64_t o_jobs = take(pl.jobs.size() * sizeof(Job));
+    const uint64_t o_items = take(pl.items.size() * sizeof(Item));
+    const uint64_t o_mitems = take(pl.n_mitems * sizeof(MergeItem));
+    const uint64_t o_ss = take(pl.seg_start.size() * sizeof(uint32_t));
+    const uint64_t o_sv = take(pl.seg_vend.size() * sizeof(uint32_t));
+    const uint64_t o_pid = take(pl.part_rows * lp * sizeof(uint32_t));
+    const uint64_t o_pd = take(pl.part_rows * lp * sizeof(float));
+    const uint64_t o_pb = take(pl.part_rows * sizeof(float));
+    const uint64_t o_fc = take(2 * sizeof(uint32_t));
+    const uint64_t o_fl = take(std::max<uint64_t>(pl.rows, 1) * sizeof(uint2));
+    if (off > UNG_HIP_NOALLOC_SCRATCH_BYTES) {
+        set_error("ung_hip_cross_topk_noalloc: the call needs %llu bytes of scratch, the maximum is %llu "
+                  "(use ung_hip_cross_topk_device)",
+                  (unsigned long long)off, (unsigned long long)UNG_HIP_NOALLOC_SCRATCH_BYTES);
+        return UNG_HIP_EINVAL;
+    }
+    unsigned char *b = ctx->scratch_dev;
+    m.jobs = reinterpret_cast<Job *>(b + o_jobs);
+    m.items = reinterpret_cast<Item *>(b + o_items);
+    m.mitems = reinterpret_cast<MergeItem *>(b + o_mitems);
+    m.seg_start = reinterpret_cast<uint32_t *>(b + o_ss);
+    m.seg_vend = reinterpret_cast<uint32_t *>(b + o_sv);
+    m.part_ids = reinterpret_cast<uint32_t *>(b + o_pid);
+    m.part_dist = reinterpret_cast<float *>(b + o_pd);
+    m.part_bound = reinterpret_cast<float *>(b + o_pb);
+    m.flag_count = reinterpret_cast<uint32_t *>(b + o_fc);
+    m.flagged = reinterpret_cast<uint2 *>(b + o_fl);
+    const uint64_t rest = UNG_HIP_NOALLOC_SCRATCH_BYTES - off;
+    m.fb_grow = false;
+    m.fb_cap = rest / (sizeof(uint32_t) + sizeof(float)) / 64 * 64;
+    m.fb_ids = reinterpret_cast<uint32_t *>(b + off);
+    m.fb_dist = reinterpret_cast<float *>(b + off + al(m.fb_cap * sizeof(uint32_t)));
+    if (off + al(m.fb_cap * sizeof(uint32_t)) + m.fb_cap * sizeof(float) > UNG_HIP_NOALLOC_SCRATCH_BYTES)
+        m.fb_cap = 0; // (alignment left too little room: one range per rescanned row)
+    return UNG_HIP_OK;
+}
+
+int check_device_ptr(const void *p, int device, const char *what)
+{
+    hipPointerAttribute_t a{};
+    if (!p || hipPointerGetAttributes(&a, p) != hipSuccess || a.type != hipMemoryTypeDevice || a.device != device) {
+        (void)hipGetLastError();
+        set_error("ung_hip_cross_topk_noalloc: %s is not device memory of device %d", what, device);
+        return UNG_HIP_EINVAL;
+    }
+    return UNG_HIP_OK;
+}
+
+int cross_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
+                  const uint32_t *out_idx, uint32_t k, uint32_t *ids, float *dist, int32_t *size, ung_hip_stats *st)
+{
+    int rc;
+    if ((rc = check_ready(ctx)))
+        return rc;
+    if (k < 1 || k > 64) {
+        set_error("k=%u outside 1..64", k);
+        return UNG_HIP_EINVAL;
+    }
+    if (!ctx->scratch_dev) {
+        set_error("ung_hip_cross_topk_noalloc: the scratch array of device %d was not resolved", ctx->device);
+        return UNG_HIP_ESTATE;
+    }
+    if ((rc = set_device(ctx)) || (rc = check_device_ptr(ids, ctx->device, "out_ids_dev")) ||
+        (rc = check_device_ptr(dist, ctx->device, "out_dist_dev")) ||
+        (rc = check_device_ptr(size, ctx->device, "out_size_dev")))
+        return rc;
+    const auto t0 = clk::now();
+    Plan &pl = ctx->plan0;
+    plan_reset(pl);
+    if ((rc = build_cross_plan(ctx, G, group_begin, out_ptr, out_idx, pl)))
+        return rc;
+    if (st)
+        st->plan_ms += ms_since(t0);
+    PlanMem m;
+    if ((rc = scratch_mem(ctx, pl, pick_lp(k, pick_lt(k)), m)))
+        return rc;
+    const size_t stage_bytes = stage_layout(pl).total;
+    if (ctx->noalloc_stage.size() < stage_bytes) // host memory, reused by later calls
+        ctx->noalloc_stage.resize(stage_bytes);
+    m.stage = ctx->noalloc_stage.data();
+    ctx->noalloc_rescanned.clear();
+    m.rescanned = &ctx->noalloc_rescanned;
+    m.out_ids = ids;
+    m.out_dist = dist;
+    m.out_size = size;
+    Workspace &ws = ctx->ws[0];
+    const uint64_t tot = ctx->N * k;
+    if (tot > 0) { // padding of the rows no job writes
+        hipLaunchKernelGGL(ung_fill_rows_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, ws.stream, ids,
+                           dist, size, ctx->N, k);
+        rc = hipGetLastError() == hipSuccess ? UNG_HIP_OK : UNG_HIP_EDEVICE;
+        if (rc)
+            set_error("ung_fill_rows_kernel launch failed");
+    }
+    if (rc || (rc = plan_launch(ctx, ws, pl, k, m, st)) || (rc = plan_finish(ctx, ws, pl, k, m, st))) {
+        drain_after_failure(ctx);
+        return rc;
+    }
+    HIPCHECK(hipStreamSynchronize(ws.stream));
+    if (st)
+        st->wall_ms += ms_since(t0);
+    return UNG_HIP_OK;
+}
+
+} // namespace
+
 extern "C" {
 
 const char *ung_hip_version(void) { return "ung_hip 0.2 (gfx950, split-bf16 MFMA pre-select + exact fp32 re-rank)"; }
@@ -1282,6 +1525,11 @@ int ung_hip_create(int device, ung_hip_ctx **out)
         set_error("stream/event creation failed: %s", hipGetErrorString(e));
         ung_hip_destroy(ctx);
         return UNG_HIP_EDEVICE;
+    }
+    int rc = resolve_scratch(device, &ctx->scratch_dev);
+    if (rc) {
+        ung_hip_destroy(ctx);
+        return rc;
     }
     *out = ctx;
     return UNG_HIP_OK;
@@ -1412,6 +1660,14 @@ int ung_hip_cross_topk(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin
     if (st)
         st->wall_ms = ms_since(t0);
     return rc;
+}
+
+int ung_hip_cross_topk_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
+                               const uint32_t *out_idx, uint32_t k, uint32_t *out_ids_dev, float *out_dist_dev,
+                               int32_t *out_size_dev, ung_hip_stats *st)
+{
+    clear_error();
+    return cross_noalloc(ctx, G, group_begin, out_ptr, out_idx, k, out_ids_dev, out_dist_dev, out_size_dev, st);
 }
 
 int ung_hip_cross_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **dist_dev)

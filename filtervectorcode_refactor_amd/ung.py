@@ -107,6 +107,18 @@ class HipContext:
                                                  C.byref(st)))
         return st.as_dict()
 
+    def cross_topk_noalloc(self, group_begin, out_ptr, out_idx, k: int, ids_dev: int, dist_dev: int,
+                           size_dev: int) -> dict:
+        """Cross edges into caller-owned device buffers (addresses of [N x k] uint32, [N x k]
+        float32, [N] int32), with no allocation in the call (ung_hip_cross_topk_noalloc)."""
+        group_begin, out_ptr = u32(group_begin), u32(out_ptr)
+        out_idx = u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
+        G = group_begin.shape[0] - 2
+        st = Stats()
+        check(self.lib.ung_hip_cross_topk_noalloc(self.h, G, ptr(group_begin), ptr(out_ptr), ptr(out_idx), k,
+                                                  ids_dev, dist_dev, size_dev, C.byref(st)))
+        return st.as_dict()
+
     def cross_intra_begin(self, group_begin, out_ptr, out_idx, k: int, grp_begin, grp_size, list_k: int) -> dict:
         """Cross edges (device-resident, complete on return) and a group kNN call left running
         on the second stream until intra_end (ung_hip_cross_intra_begin)."""

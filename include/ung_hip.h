@@ -113,6 +113,30 @@ int ung_hip_cross_topk_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *grou
                               const uint32_t *out_ptr, const uint32_t *out_idx, uint32_t k,
                               ung_hip_stats *st);
 int ung_hip_cross_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **dist_dev);
+
+/* Bytes of the per-GPU scratch array of ung_hip_cross_topk_noalloc. */
+#define UNG_HIP_NOALLOC_SCRATCH_BYTES (64ull << 20)
+
+/* Cross-group edges that allocate nothing.  No counterpart in the reference: this is for
+ * callers that cannot allocate device or pinned memory during the call -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same rows as
+ * ung_hip_cross_topk_device, written to the caller's device buffers out_ids_dev
+ * [N x k], out_dist_dev [N x k] and out_size_dev [N] (all required, device memory of the
+ * context's device; checked with hipPointerGetAttributes).  The call's work lists,
+ * partial rows and flags live in a file-scope device array of
+ * UNG_HIP_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process ends; a call
+ * whose plan needs more returns UNG_HIP_EINVAL (the message gives the bytes needed) --
+ * roughly 600k result rows with single-split unions at k = 6.  The call makes no
+ * hipMalloc, hipHostMalloc or hipFree; its host work lists reuse the context's storage.
+ * It needs the base set prepared beforehand (ung_hip_prepare_vectors, which allocates, at
+ * set-up).  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (from several host threads or contexts) race.  The rows are not kept in the context
+ * (ung_hip_additional_edges does not see them; ung_hip_rescanned_rows does not list
+ * them). */
+int ung_hip_cross_topk_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
+                               const uint32_t *out_ptr, const uint32_t *out_idx, uint32_t k,
+                               uint32_t *out_ids_dev, float *out_dist_dev, int32_t *out_size_dev,
+                               ung_hip_stats *st);
 int ung_hip_download_cross(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist,
                            int32_t *out_size, ung_hip_stats *st);
 
