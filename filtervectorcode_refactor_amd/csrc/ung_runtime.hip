@@ -102,11 +102,11 @@ struct HostBuf {
 };
 
 struct Plan {
-    std::vector<Job> jobs;
-    std::vector<Item> items;
+    ung::RawVector<Job> jobs;
+    ung::RawVector<Item> items;
     uint64_t n_mitems = 0;         // merge: MERGE_ROWS rows per block (written at launch)
     std::vector<MergeItem> pitems; // packing: MERGE_Q rows per block (group plans)
-    std::vector<uint32_t> seg_start, seg_vend;
+    ung::RawVector<uint32_t> seg_start, seg_vend;
     uint64_t part_rows = 0;
     uint64_t pairs = 0;
     uint64_t padded = 0;
@@ -274,6 +274,8 @@ struct ung_hip_ctx {
     DevBuf<unsigned long long> a_cnt;
     DevBuf<unsigned char> a_tmp;
     HostBuf a_stage;
+    // host threads of the work-list planning and staging (persistent, created at create)
+    std::unique_ptr<ung::WorkerPool> pool;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
     bool force_wide = false;
     // test hook: UNG_HIP_NO_QREG=1 at create keeps the select kernel's restaged query panel
@@ -487,6 +489,79 @@ int workspace_mem(Workspace &ws, const Plan &pl, uint32_t lp, ResultBufs &res, P
     return UNG_HIP_OK;
 }
 
+// Copies a plan's jobs and segments into the staging buffer, and its items in order of
+// decreasing cost (candidate tiles): a stable counting sort by tile count (the query
+// blocks of one split stay next to each other).  Large plans run on the worker pool:
+// per-chunk histograms, a prefix over (bucket, chunk), a scatter.
+void stage_plan(ung_hip_ctx *ctx, const Plan &pl, const StageLayout &L, char *hs)
+{
+    auto tiles = [](const Item &it) { return (it.v_end - it.v_begin + BC - 1) / BC; };
+    const uint64_t n = pl.items.size();
+    const int T = ctx->pool ? ctx->pool->size() : 1;
+    Item *sorted = reinterpret_cast<Item *>(hs + L.oi);
+    uint32_t max_t = 0;
+    if (n < 65536 || T == 1) {
+        std::memcpy(hs + L.oj, pl.jobs.data(), L.bj);
+        std::memcpy(hs + L.os, pl.seg_start.data(), L.bs);
+        std::memcpy(hs + L.ov, pl.seg_vend.data(), L.bs);
+        for (const Item &it : pl.items)
+            max_t = std::max(max_t, tiles(it));
+        std::vector<uint64_t> start(max_t + 2, 0);
+        for (const Item &it : pl.items)
+            ++start[max_t - tiles(it) + 1];
+        for (uint32_t t = 0; t <= max_t; ++t)
+            start[t + 1] += start[t];
+        for (const Item &it : pl.items)
+            sorted[start[max_t - tiles(it)]++] = it;
+        return;
+    }
+    const uint32_t nch = (uint32_t)std::min<uint64_t>(4ull * (uint64_t)T, (n + 4095) / 4096);
+    auto chunk_begin = [&](uint32_t c) { return n * c / nch; };
+    std::vector<uint32_t> cmax(nch, 0);
+    ctx->pool->run(nch, [&](int64_t c) {
+        uint32_t m = 0;
+        for (uint64_t i = chunk_begin((uint32_t)c); i < chunk_begin((uint32_t)c + 1); ++i)
+            m = std::max(m, tiles(pl.items[i]));
+        cmax[c] = m;
+    });
+    for (uint32_t m : cmax)
+        max_t = std::max(max_t, m);
+    const uint32_t nb = max_t + 1; // bucket max_t - tiles: decreasing cost first
+    std::vector<uint64_t> hist((size_t)nch * nb, 0);
+    // histograms, and the job / segment copies in pieces beside them
+    const uint32_t ncopy = (uint32_t)T;
+    ctx->pool->run(nch + 3 * ncopy, [&](int64_t task) {
+        if (task < (int64_t)nch) {
+            uint64_t *h = hist.data() + (size_t)task * nb;
+            for (uint64_t i = chunk_begin((uint32_t)task); i < chunk_begin((uint32_t)task + 1); ++i)
+                ++h[max_t - tiles(pl.items[i])];
+            return;
+        }
+        const uint32_t which = (uint32_t)(task - nch) / ncopy, piece = (uint32_t)(task - nch) % ncopy;
+        const char *src = which == 0 ? reinterpret_cast<const char *>(pl.jobs.data())
+                        : which == 1 ? reinterpret_cast<const char *>(pl.seg_start.data())
+                                     : reinterpret_cast<const char *>(pl.seg_vend.data());
+        char *dst = hs + (which == 0 ? L.oj : which == 1 ? L.os : L.ov);
+        const size_t bytes = which == 0 ? L.bj : L.bs;
+        const size_t b0 = bytes * piece / ncopy, b1 = bytes * (piece + 1) / ncopy;
+        std::memcpy(dst + b0, src + b0, b1 - b0);
+    });
+    uint64_t pos = 0;
+    for (uint32_t b = 0; b < nb; ++b)
+        for (uint32_t c = 0; c < nch; ++c) {
+            const uint64_t cnt = hist[(size_t)c * nb + b];
+            hist[(size_t)c * nb + b] = pos;
+            pos += cnt;
+        }
+    ctx->pool->run(nch, [&](int64_t c) {
+        uint64_t *h = hist.data() + (size_t)c * nb;
+        for (uint64_t i = chunk_begin((uint32_t)c); i < chunk_begin((uint32_t)c + 1); ++i) {
+            const Item &it = pl.items[i];
+            sorted[h[max_t - tiles(it)]++] = it;
+        }
+    });
+}
+
 // Runs a planned job list on workspace `ws` (its stream and events) with the memory of
 // `m`; result rows already initialised by the caller when some rows have no job.
 // plan_launch uploads the work lists and enqueues the select and merge kernels;
@@ -502,22 +577,7 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     const StageLayout L = stage_layout(pl);
     char *hs = m.stage;
     if (!pl.jobs.empty()) {
-        std::memcpy(hs + L.oj, pl.jobs.data(), L.bj);
-        std::memcpy(hs + L.os, pl.seg_start.data(), L.bs);
-        std::memcpy(hs + L.ov, pl.seg_vend.data(), L.bs);
-        // select items in order of decreasing cost (candidate tiles): a counting sort by
-        // tile count, stable (the query blocks of one split stay next to each other)
-        uint32_t max_t = 0;
-        for (const Item &it : pl.items)
-            max_t = std::max(max_t, (it.v_end - it.v_begin + BC - 1) / BC);
-        std::vector<uint64_t> start(max_t + 2, 0);
-        for (const Item &it : pl.items)
-            ++start[max_t - (it.v_end - it.v_begin + BC - 1) / BC + 1];
-        for (uint32_t t = 0; t <= max_t; ++t)
-            start[t + 1] += start[t];
-        Item *sorted = reinterpret_cast<Item *>(hs + L.oi);
-        for (const Item &it : pl.items)
-            sorted[start[max_t - (it.v_end - it.v_begin + BC - 1) / BC]++] = it;
+        stage_plan(ctx, pl, L, hs);
         HIPCHECK(hipMemcpyAsync(m.jobs, hs + L.oj, L.bj, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(m.items, hs + L.oi, L.bi, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(m.seg_start, hs + L.os, L.bs, hipMemcpyHostToDevice, ws.stream));
@@ -712,6 +772,18 @@ int check_ready(ung_hip_ctx *ctx)
     return UNG_HIP_OK;
 }
 
+// One chunk of groups of a cross plan: pass 1 counts its jobs, segments and items and
+// validates its groups; after a prefix over the chunks pass 2 writes them at its offsets.
+struct PlanChunk {
+    uint32_t g_begin = 0, g_end = 0; // groups [g_begin, g_end)
+    uint64_t jobs = 0, segs = 0, items = 0, mitems = 0, part_rows = 0, pairs = 0, padded = 0, rows = 0;
+    int rc = UNG_HIP_OK;
+    char msg[192] = {};
+};
+
+// Cross plan: one job per group C with a non-empty union of its out-groups, its segments
+// (the out-groups' ranges in LNG row order), and its items (query blocks x splits,
+// split-major).  Two passes over chunks of groups on the context's worker pool.
 int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, const uint32_t *out_ptr,
                      const uint32_t *out_idx, Plan &pl)
 {
@@ -724,66 +796,162 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
                   (unsigned long long)ctx->N);
         return UNG_HIP_EINVAL;
     }
-    for (uint32_t g = 1; g <= G; ++g) {
-        if (group_begin[g + 1] < group_begin[g]) {
-            set_error("ung_hip_cross_topk: group_begin not monotone at group %u", g);
-            return UNG_HIP_EINVAL;
-        }
-        if (out_ptr[g + 1] < out_ptr[g]) {
-            set_error("ung_hip_cross_topk: out_ptr not monotone at group %u", g);
-            return UNG_HIP_EINVAL;
+    // chunks of about equal groups + LNG entries (G small: one chunk, no thread hand-off)
+    const int T = ctx->pool ? ctx->pool->size() : 1;
+    const uint32_t nch = G < 4096 || T == 1 ? 1u : (uint32_t)std::min<uint64_t>(G, 8ull * (uint64_t)T);
+    std::vector<PlanChunk> ch(nch);
+    {
+        const uint64_t E = out_ptr[G + 1];
+        uint32_t prev = 1;
+        for (uint32_t t = 0; t < nch; ++t) {
+            ch[t].g_begin = prev;
+            uint32_t end = G + 1;
+            if (t + 1 < nch) {
+                // first group c with (c - 1) + out_ptr[c] >= the chunk's share
+                const uint64_t want = (uint64_t)(t + 1) * ((uint64_t)G + E) / nch;
+                uint32_t lo = prev, hi = G + 1;
+                while (lo < hi) {
+                    const uint32_t mid = lo + (hi - lo) / 2;
+                    if ((uint64_t)(mid - 1) + out_ptr[mid] >= want)
+                        hi = mid;
+                    else
+                        lo = mid + 1;
+                }
+                end = std::max(prev, lo);
+            }
+            ch[t].g_end = end;
+            prev = end;
         }
     }
-    // upper bounds of the list sizes: no reallocation while planning
-    pl.seg_start.reserve(out_ptr[G + 1]);
-    pl.seg_vend.reserve(out_ptr[G + 1]);
-    pl.jobs.reserve(G);
-    for (uint32_t c = 1; c <= G; ++c) {
-        const uint32_t qn = group_begin[c + 1] - group_begin[c];
-        if (qn == 0 || out_ptr[c + 1] == out_ptr[c])
-            continue;
-        Job jb{};
-        jb.q_begin = group_begin[c];
-        jb.q_count = qn;
-        jb.seg_begin = (uint32_t)pl.seg_start.size();
-        uint64_t u = 0;
-        for (uint32_t e = out_ptr[c]; e < out_ptr[c + 1]; ++e) {
-            const uint32_t x = out_idx[e];
-            if (x < 1 || x > G) {
-                set_error("ung_hip_cross_topk: out_idx entry %u out of range 1..%u", x, G);
-                return UNG_HIP_EINVAL;
-            }
-            const uint32_t nx = group_begin[x + 1] - group_begin[x];
-            if (nx == 0)
+#define PLAN_FAIL(c, ...)                                                                  \
+    do {                                                                                   \
+        (c).rc = UNG_HIP_EINVAL;                                                           \
+        std::snprintf((c).msg, sizeof((c).msg), __VA_ARGS__);                              \
+        return;                                                                            \
+    } while (0)
+    auto pass1 = [&](int64_t t) {
+        PlanChunk &c = ch[t];
+        for (uint32_t g = c.g_begin; g < c.g_end; ++g) {
+            if (group_begin[g + 1] < group_begin[g])
+                PLAN_FAIL(c, "ung_hip_cross_topk: group_begin not monotone at group %u", g);
+            if (out_ptr[g + 1] < out_ptr[g])
+                PLAN_FAIL(c, "ung_hip_cross_topk: out_ptr not monotone at group %u", g);
+            const uint32_t qn = group_begin[g + 1] - group_begin[g];
+            if (qn == 0 || out_ptr[g + 1] == out_ptr[g])
                 continue;
-            u += nx;
-            if (u >= 0xFFFFFFFFull) {
-                set_error("ung_hip_cross_topk: candidate union of group %u exceeds 2^32", c);
-                return UNG_HIP_EINVAL;
+            uint64_t u = 0, segs = 0;
+            for (uint32_t e = out_ptr[g]; e < out_ptr[g + 1]; ++e) {
+                const uint32_t x = out_idx[e];
+                if (x < 1 || x > G)
+                    PLAN_FAIL(c, "ung_hip_cross_topk: out_idx entry %u out of range 1..%u", x, G);
+                const uint32_t nx = group_begin[x + 1] - group_begin[x];
+                if (nx == 0)
+                    continue;
+                u += nx;
+                ++segs;
+                if (u >= 0xFFFFFFFFull)
+                    PLAN_FAIL(c, "ung_hip_cross_topk: candidate union of group %u exceeds 2^32", g);
             }
-            pl.seg_start.push_back(group_begin[x]);
-            pl.seg_vend.push_back((uint32_t)u);
+            if (u == 0)
+                continue;
+            const uint64_t sv = split_size(u), ns = (u + sv - 1) / sv, qb = (qn + BQ - 1) / BQ;
+            c.jobs += 1;
+            c.segs += segs;
+            c.items += ns * qb;
+            c.mitems += (qn + MERGE_ROWS - 1) / MERGE_ROWS;
+            c.part_rows += (uint64_t)qn * ns;
+            c.pairs += (uint64_t)qn * u;
+            c.rows += qn;
+            const uint64_t last = u - (ns - 1) * sv;
+            c.padded += (uint64_t)BQ * qb * ((ns - 1) * sv + (last + BC - 1) / BC * BC);
         }
-        if (u == 0)
-            continue;
-        jb.seg_count = (uint32_t)pl.seg_start.size() - jb.seg_begin;
-        jb.n_cand = (uint32_t)u;
-        jb.split_v = split_size(u);
-        jb.n_split = (uint32_t)((u + jb.split_v - 1) / jb.split_v);
-        jb.part_base = (uint32_t)pl.part_rows;
-        jb.out_row = group_begin[c];
-        jb.id_base = 0;
-        jb.flags = 0;
-        pl.part_rows += (uint64_t)qn * jb.n_split;
-        if (pl.part_rows >= 0xFFFFFFFFull) {
-            set_error("ung_hip_cross_topk: partial rows exceed 2^32");
-            return UNG_HIP_EINVAL;
+    };
+#undef PLAN_FAIL
+    if (nch == 1)
+        pass1(0);
+    else
+        ctx->pool->run(nch, pass1);
+    uint64_t n_jobs = 0, n_segs = 0, n_items = 0;
+    std::vector<uint64_t> o_job(nch), o_seg(nch), o_item(nch), o_part(nch);
+    for (uint32_t t = 0; t < nch; ++t) {
+        if (ch[t].rc) {
+            set_error("%s", ch[t].msg);
+            return ch[t].rc;
         }
-        pl.pairs += (uint64_t)qn * u;
-        pl.rows += qn;
-        pl.jobs.push_back(jb);
-        add_items_for_job(pl, (uint32_t)pl.jobs.size() - 1);
+        o_job[t] = n_jobs;
+        o_seg[t] = n_segs;
+        o_item[t] = n_items;
+        o_part[t] = pl.part_rows;
+        n_jobs += ch[t].jobs;
+        n_segs += ch[t].segs;
+        n_items += ch[t].items;
+        pl.part_rows += ch[t].part_rows;
+        pl.n_mitems += ch[t].mitems;
+        pl.pairs += ch[t].pairs;
+        pl.padded += ch[t].padded;
+        pl.rows += ch[t].rows;
     }
+    if (pl.part_rows >= 0xFFFFFFFFull || n_segs >= 0xFFFFFFFFull) {
+        set_error("ung_hip_cross_topk: partial rows exceed 2^32");
+        return UNG_HIP_EINVAL;
+    }
+    pl.jobs.resize(n_jobs);
+    pl.items.resize(n_items);
+    pl.seg_start.resize(n_segs);
+    pl.seg_vend.resize(n_segs);
+    auto pass2 = [&](int64_t t) {
+        uint64_t j = o_job[t], sg = o_seg[t], itn = o_item[t], part = o_part[t];
+        for (uint32_t g = ch[t].g_begin; g < ch[t].g_end; ++g) {
+            const uint32_t qn = group_begin[g + 1] - group_begin[g];
+            if (qn == 0 || out_ptr[g + 1] == out_ptr[g])
+                continue;
+            const uint64_t seg0 = sg;
+            uint64_t u = 0;
+            for (uint32_t e = out_ptr[g]; e < out_ptr[g + 1]; ++e) {
+                const uint32_t x = out_idx[e];
+                const uint32_t nx = group_begin[x + 1] - group_begin[x];
+                if (nx == 0)
+                    continue;
+                u += nx;
+                pl.seg_start[sg] = group_begin[x];
+                pl.seg_vend[sg] = (uint32_t)u;
+                ++sg;
+            }
+            if (u == 0)
+                continue;
+            Job jb{};
+            jb.q_begin = group_begin[g];
+            jb.q_count = qn;
+            jb.seg_begin = (uint32_t)seg0;
+            jb.seg_count = (uint32_t)(sg - seg0);
+            jb.n_cand = (uint32_t)u;
+            jb.split_v = split_size(u);
+            jb.n_split = (uint32_t)((u + jb.split_v - 1) / jb.split_v);
+            jb.part_base = (uint32_t)part;
+            jb.out_row = group_begin[g];
+            jb.id_base = 0;
+            jb.flags = 0;
+            part += (uint64_t)qn * jb.n_split;
+            pl.jobs[j] = jb;
+            // split-major: consecutive items are query blocks streaming the same candidates
+            for (uint32_t s = 0; s < jb.n_split; ++s)
+                for (uint32_t qo = 0; qo < qn; qo += BQ) {
+                    Item it{};
+                    it.job = (uint32_t)j;
+                    it.q_off = qo;
+                    it.q_cnt = std::min<uint32_t>(BQ, qn - qo);
+                    it.v_begin = s * jb.split_v;
+                    it.v_end = (uint32_t)std::min<uint64_t>(u, (uint64_t)(s + 1) * jb.split_v);
+                    it.split = s;
+                    pl.items[itn++] = it;
+                }
+            ++j;
+        }
+    };
+    if (nch == 1)
+        pass2(0);
+    else
+        ctx->pool->run(nch, pass2);
     return UNG_HIP_OK;
 }
 
@@ -1028,7 +1196,7 @@ int group_prepare_result(ung_hip_ctx *ctx, const Plan &pl, uint32_t list_k)
 int group_complete(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t list_k)
 {
     int rc;
-    ctx->group_jobs = pl.jobs;
+    ctx->group_jobs.assign(pl.jobs.begin(), pl.jobs.end());
     ctx->group_pitems = pl.pitems;
     ctx->group_list_k = list_k;
     if (!pl.jobs.empty()) {
@@ -1525,6 +1693,18 @@ int ung_hip_create(int device, ung_hip_ctx **out)
         set_error("stream/event creation failed: %s", hipGetErrorString(e));
         ung_hip_destroy(ctx);
         return UNG_HIP_EDEVICE;
+    }
+    {
+        // host threads for planning: UNG_HIP_HOST_THREADS, else OMP_NUM_THREADS, else the
+        // hardware's (at most 16)
+        int nt = 0;
+        if (const char *v = std::getenv("UNG_HIP_HOST_THREADS"))
+            nt = std::atoi(v);
+        else if (const char *v2 = std::getenv("OMP_NUM_THREADS"))
+            nt = std::atoi(v2);
+        if (nt <= 0)
+            nt = std::min(16, ung::resolve_threads(0));
+        ctx->pool = std::make_unique<ung::WorkerPool>(std::min(nt, 64));
     }
     int rc = resolve_scratch(device, &ctx->scratch_dev);
     if (rc) {
