@@ -62,5 +62,22 @@ def build(verbose: bool = True) -> str:
     return LIB_PATH
 
 
+ADAPTER_SRC = os.path.join(ROOT, "tests", "cpp", "adapter_check.cpp")
+ADAPTER_BIN = os.path.join(ROOT, "tests", "cpp", "_bin", "adapter_check")
+
+
+def build_adapter_check(verbose: bool = True) -> str:
+    """The C++ program that drives include/ung_hip_adapter.hpp against libung_hip.so
+    (run by tests/test_gpu_adapter.py); linked with a relative run path so the tree can
+    move to another machine."""
+    os.makedirs(os.path.dirname(ADAPTER_BIN), exist_ok=True)
+    tmp = ADAPTER_BIN + ".tmp"
+    _run([CXX, "-std=c++17", "-O2", "-Wall", "-I", INCLUDE, ADAPTER_SRC, "-L", HERE, "-lung_hip",
+          "-Wl,-rpath,$ORIGIN/../../../filtervectorcode_refactor_amd", "-Wl,-rpath-link,/opt/rocm/lib",
+          "-o", tmp], verbose)
+    os.replace(tmp, ADAPTER_BIN)
+    return ADAPTER_BIN
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
