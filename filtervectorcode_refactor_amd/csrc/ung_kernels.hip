@@ -1253,6 +1253,534 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
 }
 
 // ---------------------------------------------------------------------------
+// filter-and-buffer select (group kNN lists)
+// ---------------------------------------------------------------------------
+// For group kNN calls with d <= 128 whose splits hold fewer than 65,536 candidates (the
+// mid-group batch of the exact kNN stage: K = 32, Lp = 40).  ung_select_kernel needs
+// queues of LT >= K entries for such lists, and their sorted insertions (about 4.4
+// instructions per queue entry, for the wave's largest survivor count) dominate it;
+// here a survivor costs one LDS append:
+//   * each query has a buffer of up to KNN_CAP (value, candidate) entries in LDS and a
+//     threshold tau: every candidate of the split whose value is below tau is in the
+//     buffer, so no candidate at or above tau is needed again;
+//   * per tile, a lane's values that pass a branch-free pre-filter (in s-space, a
+//     superset of a < tau) are appended behind one LDS atomic per lane; the first tile
+//     (tau = +inf) appends every candidate;
+//   * when a buffer holds more than KNN_TRIG entries the block refreshes all buffers:
+//     a 64-bin histogram of a query's live entries (below tau) over [min, max] gives
+//     the bin of its (Lp+1)-th value; the buffer keeps the bins up to it (only those
+//     below it when that would be more than the limit) and tau drops to the smallest
+//     value left out (every kept value is below it: the bin is monotone in the value);
+//   * a buffer that would overflow drops the values and records the smallest, which
+//     caps tau at the next refresh, so the first point holds again;
+//   * after the last tile a final refresh keeps at most KNN_OUT entries; four threads
+//     per query sort them by value (bitonic, 16 each) and write the partial row: its Lp
+//     smallest entries and the bound min(tau, the (Lp+1)-th).
+// Every candidate left out of the row then has a value at or above the bound: the
+// partial-row contract of ung_select_kernel, whose merge, certificate and rescan follow.
+// The query operands stay in registers for the whole item (16 words per 32-dimension
+// chunk and lane), so a step loads and stages only the candidate chunk.
+constexpr int KNN_CAP = 128;              // buffer entries per query
+constexpr int KNN_VROW = KNN_CAP + 4;     // value row stride in floats (16-byte rows; bank rotation)
+constexpr int KNN_IROW = KNN_CAP + 8;     // candidate row stride in u16
+constexpr uint32_t KNN_TRIG = 80;         // a buffer above this many entries asks for a refresh
+constexpr uint32_t KNN_KEEP = 80;         // most entries a refresh keeps
+constexpr uint32_t KNN_OUT = 64;          // most entries the final refresh keeps (4 threads x 16)
+constexpr int KNN_BINS = 64;
+constexpr int KNN_THREADS = 512;          // 8 waves: 2 (candidate halves) x 4 (query quarters)
+constexpr uint32_t KNN_MAX_SPLIT = 65535; // candidates per item (16-bit candidate index)
+constexpr int KNN_MAX_NK = 4;             // dp <= 128
+
+struct alignas(16) KnnSmem {
+    float4 xs[2][BC][LDSW / 4];     // candidate chunks, double-buffered (the free half holds
+                                    // the refresh histograms: 32 words of 16-bit bins a query)
+    float bval[BQ][KNN_VROW];       // buffer values (expansion-form distances)
+    uint16_t bidx[BQ][KNN_IROW];    // their candidates (index in the item's split)
+    uint32_t rowid[3][BC];
+    uint2 nhx[3][BC];
+    float qn[BQ];
+    float tau[BQ];
+    uint32_t lost[BQ];  // order key of the smallest value a full buffer dropped
+    uint32_t fill[BQ];
+    uint32_t need;      // some buffer holds more than KNN_TRIG entries
+};
+static_assert(sizeof(float4) * BC * (LDSW / 4) >= sizeof(uint32_t) * BQ * KNN_BINS / 2,
+              "the histograms fit one panel buffer");
+static_assert(KNN_THREADS == 4 * BQ, "four threads per query in the refresh and the sort");
+
+// Unsigned key with the order of the float (negative values included).
+__device__ __forceinline__ uint32_t ord_key(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float ord_val(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// Value of lane (lane ^ X) within each group of four lanes (DPP quad permutation).
+template <int X>
+__device__ __forceinline__ uint32_t quad_xor(uint32_t v)
+{
+    static_assert(X == 1 || X == 2, "partner within the quad");
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, X == 1 ? 0xB1 : 0x4E, 0xF, 0xF, false);
+}
+template <int X>
+__device__ __forceinline__ float quad_xor(float v)
+{
+    return __uint_as_float(quad_xor<X>(__float_as_uint(v)));
+}
+__device__ __forceinline__ uint32_t quad_sum(uint32_t v)
+{
+    v += quad_xor<1>(v);
+    return v + quad_xor<2>(v);
+}
+__device__ __forceinline__ float quad_min(float v)
+{
+    v = fminf(v, quad_xor<1>(v));
+    return fminf(v, quad_xor<2>(v));
+}
+__device__ __forceinline__ float quad_max(float v)
+{
+    v = fmaxf(v, quad_xor<1>(v));
+    return fmaxf(v, quad_xor<2>(v));
+}
+// Inclusive prefix sum over the quad (lane order p = lane & 3): add lane p-1's value
+// (quad_perm [0,0,1,2]), then lane p-2's partial sum (lanes 2, 3 read lanes 0, 1).
+__device__ __forceinline__ uint32_t quad_incl(uint32_t v, int p)
+{
+    const uint32_t a = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x90, 0xF, 0xF, false);
+    v += p >= 1 ? a : 0u;
+    const uint32_t b = quad_xor<2>(v);
+    return v + (p >= 2 ? b : 0u);
+}
+
+template <int MODE, int NK>
+__global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectParams P)
+{
+    constexpr int NTH = KNN_THREADS;
+    constexpr int RSTEP = NTH / 8;  // loader row step
+    constexpr int LM = BC / RSTEP;  // candidate rows per thread and chunk
+    constexpr uint32_t DP = (uint32_t)NK * KC;
+    __shared__ KnnSmem sm;
+    __shared__ uint32_t item_slot;
+    const uint32_t logical = take_item(P.item_ctr, &item_slot);
+    if (logical >= P.n_items)
+        return;
+    const Item it = P.items[logical];
+    const Job jb = P.jobs[it.job];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / 4, wn = wave % 4;
+    const int r = lane & 31, h = lane >> 5;
+    const int col = wn * 32 + r; // this lane's query column
+    const uint32_t q0 = __builtin_amdgcn_readfirstlane(jb.q_begin + it.q_off);
+    const uint32_t qcnt = __builtin_amdgcn_readfirstlane(it.q_cnt);
+    const uint32_t ncand = it.v_end - it.v_begin;
+    const uint32_t Lp = P.lp;
+    const uint32_t *__restrict__ XS = P.xs;
+
+    if (tid < BQ) {
+        sm.qn[tid] = (uint32_t)tid < qcnt ? P.xn[q0 + tid] : 0.0f;
+        sm.tau[tid] = INFINITY;
+        sm.lost[tid] = ord_key(INFINITY);
+        sm.fill[tid] = 0u;
+    }
+    if (tid == 0)
+        sm.need = 0u;
+
+    const int lr0 = tid >> 3;
+    const int c4 = (tid & 7) * 4;
+    [[maybe_unused]] __amdgpu_buffer_rsrc_t qres, xres;
+    [[maybe_unused]] uint32_t xoff[LM];
+    [[maybe_unused]] const uint32_t *xrow[LM];
+    if constexpr (MODE == LOAD_BUF32)
+        xres = __builtin_amdgcn_make_buffer_rsrc((void *)XS, (short)0, (int)P.x_bytes, 0x00020000);
+    else
+        qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * DP), (short)0, (int)(qcnt * DP * 4u),
+                                                 0x00020000);
+    // this lane's query column for the whole item: the high and low words of every
+    // k-block (chunk kc, block kb: float4 column 2*kb + h of the chunk row, +4 for the
+    // low words); columns past the item's queries load zeros or rows never read out
+    bf16x8 qh[NK][2], ql[NK][2];
+    {
+        const __amdgpu_buffer_rsrc_t res = MODE == LOAD_BUF32 ? xres : qres;
+        const uint32_t row = (MODE == LOAD_BUF32 ? q0 : 0u) + (uint32_t)col;
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const uint32_t off = (row * DP + (uint32_t)(kc * KC + (2 * kb + h) * 4)) * 4u;
+                qh[kc][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(res, off, 0, 0));
+                ql[kc][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(res, off + 64u, 0, 0));
+            }
+    }
+    auto set_xrows = [&](int slot) {
+#pragma unroll
+        for (int m = 0; m < LM; ++m) {
+            uint32_t g = sm.rowid[slot][lr0 + RSTEP * m];
+            g = (g == NONE) ? 0u : g; // padding rows load row 0 (their -|x|^2/2 is -inf)
+            if constexpr (MODE == LOAD_BUF32)
+                xoff[m] = (g * DP + (uint32_t)c4) * 4u;
+            else
+                xrow[m] = XS + (size_t)g * DP + c4;
+        }
+    };
+    float4 rx[LM];
+    auto load_chunk = [&](uint32_t kc) {
+#pragma unroll
+        for (int m = 0; m < LM; ++m) {
+            if constexpr (MODE == LOAD_BUF32)
+                rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
+            else
+                rx[m] = __builtin_bit_cast(float4, *reinterpret_cast<const u32x4 *>(xrow[m] + kc));
+        }
+    };
+
+    const uint32_t ntiles = (ncand + BC - 1) / BC;
+    __syncthreads(); // qn and the buffer state
+    const float qnv = sm.qn[col];
+    const bool qok = (uint32_t)col < qcnt;
+    // the query's own virtual candidate index (group jobs: candidates = the queries' group)
+    const uint32_t self_v = (jb.flags & 1u) ? it.q_off + (uint32_t)col : NONE;
+    float tau_q = INFINITY; // this lane's copy of its query's threshold
+
+    // Refresh of every query's buffer (block-uniform call; four threads per query:
+    // thread p holds entries 32p .. 32p+31).  fin: the final one (at most KNN_OUT kept).
+    auto refresh = [&](bool fin, uint32_t *hist_all) __attribute__((always_inline)) {
+        const int q = tid >> 2, p = tid & 3;
+        const bool qv = (uint32_t)q < qcnt;
+        const uint32_t f = min(sm.fill[q], (uint32_t)KNN_CAP);
+        const float T0 = fminf(sm.tau[q], ord_val(sm.lost[q]));
+        float v[32];
+        uint32_t ip[16];
+#pragma unroll
+        for (int i4 = 0; i4 < 8; ++i4) {
+            const float4 x = *reinterpret_cast<const float4 *>(&sm.bval[q][32 * p + 4 * i4]);
+            v[4 * i4] = x.x;
+            v[4 * i4 + 1] = x.y;
+            v[4 * i4 + 2] = x.z;
+            v[4 * i4 + 3] = x.w;
+        }
+#pragma unroll
+        for (int i8 = 0; i8 < 4; ++i8) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(&sm.bidx[q][32 * p + 8 * i8]);
+            ip[4 * i8] = w.x;
+            ip[4 * i8 + 1] = w.y;
+            ip[4 * i8 + 2] = w.z;
+            ip[4 * i8 + 3] = w.w;
+        }
+        // live entries: written (below the fill) and below T0; the others become +inf
+        uint32_t n_own = 0u;
+        float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const bool l = qv && (uint32_t)(32 * p + i) < f && v[i] < T0;
+            v[i] = l ? v[i] : INFINITY;
+            n_own += l ? 1u : 0u;
+            mn = v[i] < mn ? v[i] : mn;
+            mx = (l && v[i] > mx) ? v[i] : mx;
+        }
+        const uint32_t n_live = quad_sum(n_own);
+        mn = quad_min(mn);
+        mx = quad_max(mx);
+        const uint32_t target = Lp + 1u;
+        const uint32_t limit = fin ? KNN_OUT : KNN_KEEP;
+        const bool hist = fin ? n_live > KNN_OUT : n_live > target;
+        uint32_t *const hq = hist_all + q * (KNN_BINS / 2);
+        if (hist) {
+            reinterpret_cast<uint4 *>(hq)[2 * p] = make_uint4(0u, 0u, 0u, 0u);
+            reinterpret_cast<uint4 *>(hq)[2 * p + 1] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        __syncthreads(); // every buffer read; `need` read by all; histograms zeroed
+        if (tid == 0)
+            sm.need = 0u;
+        const float scale = mx > mn ? (float)KNN_BINS / (mx - mn) : 0.0f;
+        auto bin_of = [&](float x) { return min((uint32_t)((x - mn) * scale), (uint32_t)(KNN_BINS - 1)); };
+        if (hist) {
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                if (v[i] < INFINITY) {
+                    const uint32_t b = bin_of(v[i]);
+                    atomicAdd(hq + (b >> 1), 1u << ((b & 1u) << 4));
+                }
+        }
+        __syncthreads(); // histograms complete
+        // kept: the live entries, or (after a histogram) those in the bins up to b* -- or
+        // below it when that would be more than the limit
+        int bkeep = KNN_BINS;
+        float tnew = T0;
+        if (hist) {
+            // this thread's 16 bins (16p .. 16p+15) and the bin of the target-th value
+            const uint4 w0 = reinterpret_cast<const uint4 *>(hq)[2 * p];
+            const uint4 w1 = reinterpret_cast<const uint4 *>(hq)[2 * p + 1];
+            const uint32_t wd[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            uint32_t sum = 0u;
+#pragma unroll
+            for (int w = 0; w < 8; ++w)
+                sum += (wd[w] & 0xFFFFu) + (wd[w] >> 16);
+            const uint32_t incl = quad_incl(sum, p);
+            uint32_t cum = incl - sum, bstar = 0u, c_le = 0u;
+            bool found = false;
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const uint32_t c = (b & 1) ? (wd[b >> 1] >> 16) : (wd[b >> 1] & 0xFFFFu);
+                const bool hit = !found && cum < target && cum + c >= target;
+                bstar = hit ? (uint32_t)(16 * p + b) : bstar;
+                c_le = hit ? cum + c : c_le;
+                found = found || hit;
+                cum += c;
+            }
+            // one thread of the quad found it (target <= n_live)
+            bstar = quad_sum(bstar);
+            c_le = quad_sum(c_le);
+            bkeep = (int)bstar - (c_le <= limit ? 0 : 1);
+        }
+        // compaction to the front of the row (the entries are all in registers)
+        uint32_t nk_ = 0u;
+        bool kp[32];
+        float tmin = INFINITY;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            kp[i] = v[i] < INFINITY && (int)bin_of(v[i]) <= bkeep;
+            nk_ += kp[i] ? 1u : 0u;
+            tmin = (v[i] < INFINITY && !kp[i] && v[i] < tmin) ? v[i] : tmin;
+        }
+        if (hist)
+            tnew = fminf(T0, quad_min(tmin));
+        const uint32_t kincl = quad_incl(nk_, p);
+        uint32_t pos = kincl - nk_;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (kp[i]) {
+                sm.bval[q][pos] = v[i];
+                sm.bidx[q][pos] = (uint16_t)(ip[i >> 1] >> ((i & 1) << 4));
+            }
+            pos += kp[i] ? 1u : 0u;
+        }
+        if (p == 3) {
+            sm.fill[q] = kincl;
+            sm.tau[q] = tnew;
+            sm.lost[q] = ord_key(INFINITY);
+        }
+        __syncthreads(); // buffers, fills and thresholds visible
+    };
+
+    RowCursor cur;
+    finish_rowids(sm, 0, start_rowids(sm, 0, cur, P, jb, it.v_begin, it.v_end, tid), tid);
+    __syncthreads();
+    set_xrows(0);
+    load_chunk(0);
+    floatx16 acc[2];
+    int slot = 0;
+    uint32_t s = 0; // steps done
+    for (uint32_t tile = 0; tile < ntiles; ++tile) {
+        const int next_slot = slot == 2 ? 0 : slot + 1;
+        const bool more = tile + 1 < ntiles;
+        float pend_nx = INFINITY;
+        // the tile's chunks: panels double-buffered in LDS, the next chunk (also the next
+        // tile's first) prefetched into registers, the next tile's row ids built in ring
+        // slot (tile+1)%3 meanwhile
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) {
+            const int buf = (int)((s + (uint32_t)kc) & 1u);
+#pragma unroll
+            for (int m = 0; m < LM; ++m)
+                sm.xs[buf][lr0 + RSTEP * m][c4 >> 2] = rx[m];
+            if (NK == 1 && more)
+                finish_rowids(sm, next_slot,
+                              start_rowids(sm, next_slot, cur, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid), tid);
+            if (NK > 1 && kc == 1 && more)
+                finish_rowids(sm, next_slot, pend_nx, tid);
+            __syncthreads();
+            if (kc + 1 < NK) {
+                load_chunk((uint32_t)(kc + 1) * KC);
+            } else if (more) {
+                set_xrows(next_slot);
+                load_chunk(0);
+            }
+            // three bf16 passes per 16-dimension block (hi*hi, hi*lo, lo*hi); the tile's
+            // first MFMA of each accumulator takes C = 0
+            __builtin_amdgcn_s_setprio(1);
+            const floatx16 zero = {};
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int ch = 2 * kb + h;
+                bf16x8 ah[2], al[2];
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    ah[mb] = __builtin_bit_cast(bf16x8, sm.xs[buf][wm * 64 + 32 * mb + r][ch]);
+                    al[mb] = __builtin_bit_cast(bf16x8, sm.xs[buf][wm * 64 + 32 * mb + r][ch + 4]);
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[mb], qh[kc][kb],
+                                                                      (kc == 0 && kb == 0) ? zero : acc[mb], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[mb], ql[kc][kb], acc[mb], 0, 0, 0);
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[mb], qh[kc][kb], acc[mb], 0, 0, 0);
+            }
+            __builtin_amdgcn_s_setprio(0);
+            if (NK > 1 && kc == 0 && more)
+                pend_nx = start_rowids(sm, next_slot, cur, P, jb, it.v_begin + (tile + 1) * BC, it.v_end, tid);
+        }
+        s += (uint32_t)NK;
+        // -|x|^2/2 of the candidate row by one more MFMA (three exact bf16 terms against
+        // ones): acc = -s, s = |x|^2/2 - <x,q>  (padding rows: -inf)
+        {
+            const bf16x8 bone = __builtin_bit_cast(
+                bf16x8, make_uint4(h == 0 ? 0x3F803F80u : 0u, h == 0 ? 0x00003F80u : 0u, 0u, 0u));
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+                const uint2 w = sm.nhx[slot][wm * 64 + 32 * mb + r];
+                const bf16x8 abias = __builtin_bit_cast(bf16x8, make_uint4(h == 0 ? w.x : 0u, h == 0 ? w.y : 0u, 0u, 0u));
+                acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bone, acc[mb], 0, 0, 0);
+            }
+        }
+        // the lane's values below tau into its query's buffer.  Bit 31-j of the masks is
+        // value j (row tile_row(wm, h, j)); rows past the split and the query itself are
+        // never candidates.
+        {
+            const uint32_t base_row = (uint32_t)(wm * 64 + 4 * h);
+            const uint32_t tile_v = tile * BC;
+            const int dv = (int)min(ncand - tile_v, (uint32_t)BC) - (int)base_row;
+            const uint32_t nv = dv <= 0 ? 0u : min(32u, 4u * ((uint32_t)dv >> 3) + min((uint32_t)dv & 7u, 4u));
+            uint32_t valid = nv == 0u ? 0u : (0xFFFFFFFFu << (32u - nv));
+            const int o = (int)(self_v - it.v_begin - tile_v) - (int)base_row;
+            const uint32_t sj = self_v != NONE ? lane_index_of(o) : 32u;
+            valid &= sj < 32u ? ~(0x80000000u >> sj) : 0xFFFFFFFFu;
+            valid = qok ? valid : 0u;
+            // s < c  <=>  the sign bit of -c - acc  (c = +inf: every finite value)
+            const float ncth = -s_bound(tau_q, qnv);
+            uint32_t mask = 0u;
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    mask = (mask << 1) | (__float_as_uint(ncth - acc[mb][i]) >> 31);
+            mask &= valid;
+            if (__ballot(mask != 0u)) {
+                const uint32_t cnt = (uint32_t)__popc(mask);
+                const uint32_t base = cnt ? atomicAdd(&sm.fill[col], cnt) : 0u;
+                if (base + cnt > KNN_TRIG)
+                    sm.need = 1u;
+                float *const vrow = &sm.bval[col][0];
+                uint16_t *const irow = &sm.bidx[col][0];
+                const uint32_t vbase = tile_v + base_row;
+                if (__ballot(base + cnt > (uint32_t)KNN_CAP) == 0) {
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) {
+                        if ((int)(mask << j) < 0) {
+                            const uint32_t pos = base + (uint32_t)__popc(mask & ~(0xFFFFFFFFu >> j));
+                            vrow[pos] = __builtin_fmaf(-2.0f, acc[j >> 4][j & 15], qnv);
+                            irow[pos] = (uint16_t)(vbase + (((uint32_t)j & 28u) << 1) + ((uint32_t)j & 3u));
+                        }
+                    }
+                } else {
+                    // a full buffer: the values past its capacity are dropped, the
+                    // smallest of them caps tau at the next refresh
+                    uint32_t lk = ord_key(INFINITY);
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) {
+                        if ((int)(mask << j) < 0) {
+                            const uint32_t pos = base + (uint32_t)__popc(mask & ~(0xFFFFFFFFu >> j));
+                            const float a = __builtin_fmaf(-2.0f, acc[j >> 4][j & 15], qnv);
+                            if (pos < (uint32_t)KNN_CAP) {
+                                vrow[pos] = a;
+                                irow[pos] = (uint16_t)(vbase + (((uint32_t)j & 28u) << 1) + ((uint32_t)j & 3u));
+                            } else {
+                                lk = min(lk, ord_key(a));
+                            }
+                        }
+                    }
+                    if (lk != ord_key(INFINITY))
+                        atomicMin(&sm.lost[col], lk);
+                }
+            }
+        }
+        __syncthreads(); // appends done; the panel buffer of the tile's last step is free
+        if (sm.need != 0u || !more)
+            refresh(!more, reinterpret_cast<uint32_t *>(&sm.xs[(s - 1u) & 1u][0][0]));
+        tau_q = sm.tau[col];
+        slot = next_slot;
+    }
+
+    // per query (four threads): bitonic sort of its <= KNN_OUT entries by value over
+    // elements e = 16p + i, then the partial row and its bound
+    {
+        const int q = tid >> 2, p = tid & 3;
+        const uint32_t f = sm.fill[q];
+        float d[16];
+        uint32_t id[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t e = (uint32_t)(16 * p + i);
+            const bool in = e < f;
+            d[i] = in ? sm.bval[q][e] : INFINITY;
+            id[i] = in ? (uint32_t)sm.bidx[q][e] : NONE;
+        }
+#pragma unroll
+        for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                if (j >= 16) {
+                    // partner element e ^ j: same slot of quad lane p ^ (j/16)
+                    const bool asc = ((16 * p) & k) == 0;
+                    const bool lower = ((16 * p) & j) == 0;
+                    const bool keep_min = lower == asc;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const float pd = j == 16 ? quad_xor<1>(d[i]) : quad_xor<2>(d[i]);
+                        const uint32_t pi = j == 16 ? quad_xor<1>(id[i]) : quad_xor<2>(id[i]);
+                        const bool take = keep_min ? pd < d[i] : pd > d[i];
+                        d[i] = take ? pd : d[i];
+                        id[i] = take ? pi : id[i];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int l = i ^ j;
+                        if (l > i) {
+                            // ascending pairs put the smaller value first
+                            const bool asc = k < 16 ? (i & k) == 0 : ((16 * p) & k) == 0;
+                            const bool sw = asc ? d[l] < d[i] : d[i] < d[l];
+                            const float di = d[i], dl = d[l];
+                            const uint32_t ii = id[i], il = id[l];
+                            d[i] = sw ? dl : di;
+                            d[l] = sw ? di : dl;
+                            id[i] = sw ? il : ii;
+                            id[l] = sw ? ii : il;
+                        }
+                    }
+                }
+            }
+        float next = INFINITY; // the (Lp+1)-th entry (Lp < KNN_OUT)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            next = (uint32_t)(16 * p + i) == Lp ? d[i] : next;
+        next = quad_min(next);
+        if ((uint32_t)q < qcnt) {
+            const size_t prow = (size_t)jb.part_base + (size_t)it.split * jb.q_count + it.q_off + (uint32_t)q;
+            const uint32_t id0 = P.seg_start[jb.seg_begin] + it.v_begin; // group jobs: one segment
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t e = (uint32_t)(16 * p + i);
+                if (e < Lp) {
+                    P.part_ids[prow * Lp + e] = d[i] < INFINITY ? id0 + id[i] : NONE;
+                    P.part_dist[prow * Lp + e] = d[i];
+                }
+            }
+            if (p == 0)
+                P.part_bound[prow] = fminf(sm.tau[q], next);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // merge + certification
 // ---------------------------------------------------------------------------
 struct MergeParams {

@@ -111,6 +111,7 @@ struct Plan {
     uint64_t pairs = 0;
     uint64_t padded = 0;
     uint64_t rows = 0;
+    uint64_t max_item_cand = 0;    // largest candidate range of an item
 };
 
 struct ResultBufs {
@@ -278,6 +279,9 @@ struct ung_hip_ctx {
     std::unique_ptr<ung::WorkerPool> pool;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
     bool force_wide = false;
+    // UNG_HIP_NO_KNN=1 at create sends every group kNN call through ung_select_kernel (the
+    // register-queue select) instead of the filter-and-buffer ung_knn_select_kernel
+    bool knn = true;
     // test hook: UNG_HIP_NO_QREG=1 at create keeps the select kernel's restaged query panel
     // where the register-query layout would apply
     bool qreg = true;
@@ -312,6 +316,7 @@ void plan_reset(Plan &pl)
     pl.seg_start.clear();
     pl.seg_vend.clear();
     pl.n_mitems = 0;
+    pl.max_item_cand = 0;
     pl.part_rows = 0;
     pl.pairs = 0;
     pl.padded = 0;
@@ -425,6 +430,50 @@ int launch_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P,
         HIPCHECK(hipGetLastError());
     }
     return UNG_HIP_OK;
+}
+
+// Filter-and-buffer select of a group plan (ung_knn_select_kernel, dp <= 128), grid
+// chunked like launch_select_t.
+template <int NK>
+int launch_knn_select_t(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P, uint32_t n_items)
+{
+    const uint64_t x_bytes = (uint64_t)ctx->N * ctx->dp * sizeof(uint32_t);
+    const int mode = (x_bytes < (1ull << 32) && !ctx->force_wide) ? LOAD_BUF32 : LOAD_WIDE;
+    const uint32_t max_grid = 1u << 30;
+    for (uint32_t off = 0; off < n_items; off += max_grid) {
+        SelectParams Q = P;
+        Q.items = P.items + off;
+        Q.x_bytes = mode == LOAD_BUF32 ? (uint32_t)x_bytes : 0u;
+        const uint32_t n = std::min(max_grid, n_items - off);
+        Q.n_items = n;
+        if (off > 0) {
+            hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, stream, P.item_ctr, 1u);
+            HIPCHECK(hipGetLastError());
+        }
+        if (mode == LOAD_BUF32)
+            hipLaunchKernelGGL((ung_knn_select_kernel<LOAD_BUF32, NK>), dim3(n), dim3(KNN_THREADS), 0, stream, Q);
+        else
+            hipLaunchKernelGGL((ung_knn_select_kernel<LOAD_WIDE, NK>), dim3(n), dim3(KNN_THREADS), 0, stream, Q);
+        HIPCHECK(hipGetLastError());
+    }
+    return UNG_HIP_OK;
+}
+
+int launch_knn_select(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &P, uint32_t n_items)
+{
+    switch (ctx->dp / KC) {
+    case 1:
+        return launch_knn_select_t<1>(ctx, stream, P, n_items);
+    case 2:
+        return launch_knn_select_t<2>(ctx, stream, P, n_items);
+    case 3:
+        return launch_knn_select_t<3>(ctx, stream, P, n_items);
+    case 4:
+        return launch_knn_select_t<4>(ctx, stream, P, n_items);
+    default:
+        set_error("filter-and-buffer select: dp=%u above %d", ctx->dp, KNN_MAX_NK * KC);
+        return UNG_HIP_EINVAL;
+    }
 }
 
 // Error factor of the expansion-form value a = fl(|q|^2 - 2*acc) of the select kernel:
@@ -614,7 +663,13 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     P.lp = lp;
     const uint32_t n_items = (uint32_t)pl.items.size();
     const bool excl = (pl.jobs[0].flags & 1u) != 0; // one kind of job per plan
-    if (lt == 8)
+    // group kNN lists with partial rows below 64 entries, splits below 65,536 candidates
+    // and d <= 128 (the mid-group batch of the exact kNN stage): the filter-and-buffer select
+    const bool knn = ctx->knn && excl && lp + 1u <= KNN_OUT && pl.max_item_cand <= KNN_MAX_SPLIT &&
+                     ctx->dp <= (uint32_t)(KNN_MAX_NK * KC);
+    if (knn)
+        rc = launch_knn_select(ctx, ws.stream, P, n_items);
+    else if (lt == 8)
         rc = launch_select_t<8>(ctx, ws.stream, P, n_items, excl);
     else if (lt == 16)
         rc = launch_select_t<16>(ctx, ws.stream, P, n_items, excl);
@@ -1158,6 +1213,7 @@ int build_group_plan(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_be
         // spread it over the chip, and splits would multiply its partial rows
         jb.split_v = (n + BQ - 1) / BQ >= 256 ? n : split_size(n);
         jb.n_split = (n + jb.split_v - 1) / jb.split_v;
+        pl.max_item_cand = std::max<uint64_t>(pl.max_item_cand, std::min(jb.split_v, n));
         jb.part_base = (uint32_t)pl.part_rows;
         jb.out_row = (uint32_t)row;
         jb.id_base = grp_begin[g];
@@ -1668,6 +1724,8 @@ int ung_hip_create(int device, ung_hip_ctx **out)
         ctx->force_wide = s[0] == '1';
     if (const char *s = std::getenv("UNG_HIP_NO_QREG"))
         ctx->qreg = s[0] != '1';
+    if (const char *s = std::getenv("UNG_HIP_NO_KNN"))
+        ctx->knn = s[0] != '1';
     if (const char *s = std::getenv("UNG_HIP_EPS_SCALE")) {
         const double v = std::atof(s);
         ctx->eps_scale = v >= 1.0 ? v : 1.0; // a smaller bound would not be an error bound
