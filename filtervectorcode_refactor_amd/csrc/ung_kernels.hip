@@ -1266,11 +1266,13 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
 //   * per tile, a lane's values that pass a branch-free pre-filter (in s-space, a
 //     superset of a < tau) are appended behind one LDS atomic per lane; the first tile
 //     (tau = +inf) appends every candidate;
-//   * when a buffer holds more than KNN_TRIG entries the block refreshes all buffers:
-//     a 64-bin histogram of a query's live entries (below tau) over [min, max] gives
-//     the bin of its (Lp+1)-th value; the buffer keeps the bins up to it (only those
-//     below it when that would be more than the limit) and tau drops to the smallest
-//     value left out (every kept value is below it: the bin is monotone in the value);
+//   * when a buffer holds more than KNN_TRIG entries (KNN_TRIG_LATE from the third tile
+//     on, when far fewer values pass) the block refreshes all buffers: a 64-bin
+//     histogram of a query's live entries (below tau) over [min, max], counted in
+//     registers, gives the bin of its (Lp+1)-th value; the buffer keeps the bins up to
+//     it (only those below it when that would be more than the limit) and tau drops to
+//     the smallest value left out (every kept value is below it: the bin is monotone in
+//     the value);
 //   * a buffer that would overflow drops the values and records the smallest, which
 //     caps tau at the next refresh, so the first point holds again;
 //   * after the last tile a final refresh keeps at most KNN_OUT entries; four threads
@@ -1283,17 +1285,16 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
 constexpr int KNN_CAP = 128;              // buffer entries per query
 constexpr int KNN_VROW = KNN_CAP + 4;     // value row stride in floats (16-byte rows; bank rotation)
 constexpr int KNN_IROW = KNN_CAP + 8;     // candidate row stride in u16
-constexpr uint32_t KNN_TRIG = 80;         // a buffer above this many entries asks for a refresh
+constexpr uint32_t KNN_TRIG = 80;         // a buffer above this many entries asks for a refresh (tiles 0, 1)
+constexpr uint32_t KNN_TRIG_LATE = 100;   // from tile 2 on (fewer values pass a tile)
 constexpr uint32_t KNN_KEEP = 80;         // most entries a refresh keeps
 constexpr uint32_t KNN_OUT = 64;          // most entries the final refresh keeps (4 threads x 16)
-constexpr int KNN_BINS = 64;
 constexpr int KNN_THREADS = 512;          // 8 waves: 2 (candidate halves) x 4 (query quarters)
 constexpr uint32_t KNN_MAX_SPLIT = 65535; // candidates per item (16-bit candidate index)
 constexpr int KNN_MAX_NK = 4;             // dp <= 128
 
 struct alignas(16) KnnSmem {
-    float4 xs[2][BC][LDSW / 4];     // candidate chunks, double-buffered (the free half holds
-                                    // the refresh histograms: 32 words of 16-bit bins a query)
+    float4 xs[2][BC][LDSW / 4];     // candidate chunks, double-buffered
     float bval[BQ][KNN_VROW];       // buffer values (expansion-form distances)
     uint16_t bidx[BQ][KNN_IROW];    // their candidates (index in the item's split)
     uint32_t rowid[3][BC];
@@ -1302,10 +1303,8 @@ struct alignas(16) KnnSmem {
     float tau[BQ];
     uint32_t lost[BQ];  // order key of the smallest value a full buffer dropped
     uint32_t fill[BQ];
-    uint32_t need;      // some buffer holds more than KNN_TRIG entries
+    uint32_t need[2];   // by tile parity: some buffer passed its refresh trigger
 };
-static_assert(sizeof(float4) * BC * (LDSW / 4) >= sizeof(uint32_t) * BQ * KNN_BINS / 2,
-              "the histograms fit one panel buffer");
 static_assert(KNN_THREADS == 4 * BQ, "four threads per query in the refresh and the sort");
 
 // Unsigned key with the order of the float (negative values included).
@@ -1387,8 +1386,8 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
         sm.lost[tid] = ord_key(INFINITY);
         sm.fill[tid] = 0u;
     }
-    if (tid == 0)
-        sm.need = 0u;
+    if (tid < 2)
+        sm.need[tid] = 0u;
 
     const int lr0 = tid >> 3;
     const int c4 = (tid & 7) * 4;
@@ -1444,11 +1443,14 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
     const bool qok = (uint32_t)col < qcnt;
     // the query's own virtual candidate index (group jobs: candidates = the queries' group)
     const uint32_t self_v = (jb.flags & 1u) ? it.q_off + (uint32_t)col : NONE;
-    float tau_q = INFINITY; // this lane's copy of its query's threshold
 
-    // Refresh of every query's buffer (block-uniform call; four threads per query:
-    // thread p holds entries 32p .. 32p+31).  fin: the final one (at most KNN_OUT kept).
-    auto refresh = [&](bool fin, uint32_t *hist_all) __attribute__((always_inline)) {
+    // Refresh of every query's buffer (block-uniform call; four threads per query, one
+    // quad of a wave, read and write its row, so no block barrier is needed; thread p
+    // holds entries 32p .. 32p+31).  fin: the final one (at most KNN_OUT kept).  The
+    // (Lp+1)-th live value is located by a 64-bin key K = min(floor(t * 64), 63),
+    // t = (v - min) / (max - min), monotone in v: 8 bins of K/8 with byte counters in
+    // registers summed over the quad, then the 8 sub-bins K%8 of the bin that holds it.
+    auto refresh = [&](bool fin) __attribute__((always_inline)) {
         const int q = tid >> 2, p = tid & 3;
         const bool qv = (uint32_t)q < qcnt;
         const uint32_t f = min(sm.fill[q], (uint32_t)KNN_CAP);
@@ -1473,82 +1475,102 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
         }
         // live entries: written (below the fill) and below T0; the others become +inf
         uint32_t n_own = 0u;
-        float mn = INFINITY, mx = -INFINITY;
+        float mn = INFINITY;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             const bool l = qv && (uint32_t)(32 * p + i) < f && v[i] < T0;
             v[i] = l ? v[i] : INFINITY;
             n_own += l ? 1u : 0u;
             mn = v[i] < mn ? v[i] : mn;
-            mx = (l && v[i] > mx) ? v[i] : mx;
         }
         const uint32_t n_live = quad_sum(n_own);
         mn = quad_min(mn);
-        mx = quad_max(mx);
+        // the window's top: T0 bounds every live entry once it is finite (the first
+        // refresh of an item takes the largest live entry)
+        float mx = T0;
+        if (!(T0 < INFINITY)) {
+            mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 32; ++i)
+                mx = (v[i] < INFINITY && v[i] > mx) ? v[i] : mx;
+            mx = quad_max(mx);
+        }
         const uint32_t target = Lp + 1u;
         const uint32_t limit = fin ? KNN_OUT : KNN_KEEP;
         const bool hist = fin ? n_live > KNN_OUT : n_live > target;
-        uint32_t *const hq = hist_all + q * (KNN_BINS / 2);
-        if (hist) {
-            reinterpret_cast<uint4 *>(hq)[2 * p] = make_uint4(0u, 0u, 0u, 0u);
-            reinterpret_cast<uint4 *>(hq)[2 * p + 1] = make_uint4(0u, 0u, 0u, 0u);
-        }
-        __syncthreads(); // every buffer read; `need` read by all; histograms zeroed
-        if (tid == 0)
-            sm.need = 0u;
-        const float scale = mx > mn ? (float)KNN_BINS / (mx - mn) : 0.0f;
-        auto bin_of = [&](float x) { return min((uint32_t)((x - mn) * scale), (uint32_t)(KNN_BINS - 1)); };
-        if (hist) {
+        // keys (s8 = 8 * s1 exactly, so K / 8 is the 8-bin index of t), four bytes a word
+        const float s1 = mx > mn ? 8.0f / (mx - mn) : 0.0f;
+        const float s8 = s1 * 8.0f;
+        uint32_t kw[8];
 #pragma unroll
-            for (int i = 0; i < 32; ++i)
-                if (v[i] < INFINITY) {
-                    const uint32_t b = bin_of(v[i]);
-                    atomicAdd(hq + (b >> 1), 1u << ((b & 1u) << 4));
-                }
-        }
-        __syncthreads(); // histograms complete
-        // kept: the live entries, or (after a histogram) those in the bins up to b* -- or
-        // below it when that would be more than the limit
-        int bkeep = KNN_BINS;
-        float tnew = T0;
-        if (hist) {
-            // this thread's 16 bins (16p .. 16p+15) and the bin of the target-th value
-            const uint4 w0 = reinterpret_cast<const uint4 *>(hq)[2 * p];
-            const uint4 w1 = reinterpret_cast<const uint4 *>(hq)[2 * p + 1];
-            const uint32_t wd[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-            uint32_t sum = 0u;
+        for (int w = 0; w < 8; ++w)
+            kw[w] = 0u;
 #pragma unroll
-            for (int w = 0; w < 8; ++w)
-                sum += (wd[w] & 0xFFFFu) + (wd[w] >> 16);
-            const uint32_t incl = quad_incl(sum, p);
-            uint32_t cum = incl - sum, bstar = 0u, c_le = 0u;
+        for (int i = 0; i < 32; ++i)
+            kw[i >> 2] |= min((uint32_t)((v[i] - mn) * s8), 63u) << ((i & 3) << 3);
+        auto key = [&](int i) { return (kw[i >> 2] >> ((i & 3) << 3)) & 0xFFu; };
+        // kept: the live entries with a key below kkey (every live entry without a
+        // histogram); kkey: past the key of the target-th value, or that key itself when
+        // keeping its bin would be more than the limit
+        uint32_t kkey = 64u;
+        if (hist) {
+            // byte b&3 of c[b>>2]: live entries with K/8 = b (at most 128: no carries)
+            uint32_t c0 = 0u, c1 = 0u;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const uint32_t k = key(i);
+                const uint32_t inc = v[i] < INFINITY ? 1u << (((k >> 3) & 3u) << 3) : 0u;
+                c0 += k < 32u ? inc : 0u;
+                c1 += k < 32u ? 0u : inc;
+            }
+            c0 = quad_sum(c0);
+            c1 = quad_sum(c1);
+            uint32_t cum = 0u, b1 = 0u, c_lt = 0u;
             bool found = false;
 #pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const uint32_t c = (b & 1) ? (wd[b >> 1] >> 16) : (wd[b >> 1] & 0xFFFFu);
-                const bool hit = !found && cum < target && cum + c >= target;
-                bstar = hit ? (uint32_t)(16 * p + b) : bstar;
-                c_le = hit ? cum + c : c_le;
+            for (int b = 0; b < 8; ++b) {
+                const uint32_t c = ((b < 4 ? c0 : c1) >> ((b & 3) << 3)) & 0xFFu;
+                const bool hit = !found && cum + c >= target;
+                b1 = hit ? (uint32_t)b : b1;
+                c_lt = hit ? cum : c_lt;
                 found = found || hit;
                 cum += c;
             }
-            // one thread of the quad found it (target <= n_live)
-            bstar = quad_sum(bstar);
-            c_le = quad_sum(c_le);
-            bkeep = (int)bstar - (c_le <= limit ? 0 : 1);
+            uint32_t d0 = 0u, d1 = 0u;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const uint32_t k = key(i);
+                const uint32_t inc = (v[i] < INFINITY && (k >> 3) == b1) ? 1u << ((k & 3u) << 3) : 0u;
+                d0 += (k & 4u) ? 0u : inc;
+                d1 += (k & 4u) ? inc : 0u;
+            }
+            d0 = quad_sum(d0);
+            d1 = quad_sum(d1);
+            uint32_t cum2 = c_lt, b2 = 0u, c_le = 0u;
+            found = false;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const uint32_t c = ((b < 4 ? d0 : d1) >> ((b & 3) << 3)) & 0xFFu;
+                const bool hit = !found && cum2 + c >= target;
+                b2 = hit ? (uint32_t)b : b2;
+                c_le = hit ? cum2 + c : c_le;
+                found = found || hit;
+                cum2 += c;
+            }
+            kkey = 8u * b1 + b2 + (c_le <= limit ? 1u : 0u);
         }
-        // compaction to the front of the row (the entries are all in registers)
+        // compaction to the front of the row (the entries are all in registers); tau
+        // drops to the smallest live value left out (every kept value is below it)
         uint32_t nk_ = 0u;
         bool kp[32];
         float tmin = INFINITY;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            kp[i] = v[i] < INFINITY && (int)bin_of(v[i]) <= bkeep;
+            kp[i] = v[i] < INFINITY && key(i) < kkey;
             nk_ += kp[i] ? 1u : 0u;
             tmin = (v[i] < INFINITY && !kp[i] && v[i] < tmin) ? v[i] : tmin;
         }
-        if (hist)
-            tnew = fminf(T0, quad_min(tmin));
+        const float tnew = hist ? fminf(T0, quad_min(tmin)) : T0;
         const uint32_t kincl = quad_incl(nk_, p);
         uint32_t pos = kincl - nk_;
 #pragma unroll
@@ -1564,7 +1586,6 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
             sm.tau[q] = tnew;
             sm.lost[q] = ord_key(INFINITY);
         }
-        __syncthreads(); // buffers, fills and thresholds visible
     };
 
     RowCursor cur;
@@ -1654,8 +1675,9 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
             const uint32_t sj = self_v != NONE ? lane_index_of(o) : 32u;
             valid &= sj < 32u ? ~(0x80000000u >> sj) : 0xFFFFFFFFu;
             valid = qok ? valid : 0u;
-            // s < c  <=>  the sign bit of -c - acc  (c = +inf: every finite value)
-            const float ncth = -s_bound(tau_q, qnv);
+            // s < c  <=>  the sign bit of -c - acc  (c = +inf: every finite value); tau as
+            // the latest refresh left it (visible after this tile's step barriers)
+            const float ncth = -s_bound(sm.tau[col], qnv);
             uint32_t mask = 0u;
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb)
@@ -1666,8 +1688,8 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
             if (__ballot(mask != 0u)) {
                 const uint32_t cnt = (uint32_t)__popc(mask);
                 const uint32_t base = cnt ? atomicAdd(&sm.fill[col], cnt) : 0u;
-                if (base + cnt > KNN_TRIG)
-                    sm.need = 1u;
+                if (base + cnt > (tile < 2u ? KNN_TRIG : KNN_TRIG_LATE))
+                    sm.need[tile & 1u] = 1u;
                 float *const vrow = &sm.bval[col][0];
                 uint16_t *const irow = &sm.bidx[col][0];
                 const uint32_t vbase = tile_v + base_row;
@@ -1702,15 +1724,20 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
                 }
             }
         }
-        __syncthreads(); // appends done; the panel buffer of the tile's last step is free
-        if (sm.need != 0u || !more)
-            refresh(!more, reinterpret_cast<uint32_t *>(&sm.xs[(s - 1u) & 1u][0][0]));
-        tau_q = sm.tau[col];
+        __syncthreads(); // appends done
+        // the next tile's flag is cleared here: it is set only after the next tile's step
+        // barriers, and read only after its append barrier
+        const bool do_refresh = sm.need[tile & 1u] != 0u || !more;
+        if (tid == 0)
+            sm.need[(tile + 1u) & 1u] = 0u;
+        if (do_refresh)
+            refresh(!more);
         slot = next_slot;
     }
 
     // per query (four threads): bitonic sort of its <= KNN_OUT entries by value over
     // elements e = 16p + i, then the partial row and its bound
+    __syncthreads();
     {
         const int q = tid >> 2, p = tid & 3;
         const uint32_t f = sm.fill[q];
