@@ -40,8 +40,6 @@ constexpr uint32_t MAX_SPLITS = 64; // one wave lane per split in the merge
 constexpr uint32_t MERGE_ROWS = 4;  // result rows (one wave each) per merge block
 constexpr uint32_t MERGE_Q = 256;   // rows per packing block
 constexpr uint32_t NONE = 0xFFFFFFFFu;
-constexpr uint32_t FALLBACK_RANGE = 2048;      // fewest candidates per range of a flagged row's exact rescan
-constexpr uint32_t MAX_FALLBACK_SPLITS = 1024; // most ranges per flagged row
 
 struct Job {
     uint32_t q_begin, q_count;     // queries: global ids [q_begin, q_begin+q_count)
@@ -2089,7 +2087,7 @@ struct FallbackParams {
     const uint32_t *seg_vend;
     const uint32_t *flag_count;
     const uint2 *flagged;
-    uint32_t splits;     // ranges per flagged row (1..MAX_FALLBACK_SPLITS)
+    uint32_t splits;     // ranges per flagged row (at least 1)
     uint32_t *part_ids;  // [flagged x splits x k] global ids (splits > 1)
     float *part_dist;
     uint32_t *out_ids;

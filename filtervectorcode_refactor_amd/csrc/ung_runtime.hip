@@ -719,6 +719,12 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     return UNG_HIP_OK;
 }
 
+// Exact rescan of flagged rows: a row's union is cut into ranges of at least
+// FALLBACK_RANGE candidates, at most MAX_FALLBACK_SPLITS of them, one wave each (a few
+// rows with small unions still spread over a few hundred waves).
+constexpr uint32_t FALLBACK_RANGE = 256;
+constexpr uint32_t MAX_FALLBACK_SPLITS = 1024;
+
 int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, PlanMem &m, ung_hip_stats *st)
 {
     int rc;
