@@ -1267,10 +1267,10 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
 //   * when a buffer holds more than KNN_TRIG entries (KNN_TRIG_LATE from the third tile
 //     on, when far fewer values pass) the block refreshes all buffers: a 64-bin
 //     histogram of a query's live entries (below tau) over [min, max], counted in
-//     registers, gives the bin of its (Lp+1)-th value; the buffer keeps the bins up to
-//     it (only those below it when that would be more than the limit) and tau drops to
-//     the smallest value left out (every kept value is below it: the bin is monotone in
-//     the value);
+//     registers (refined into 8 parts when the bin alone would pass the limit), gives
+//     the bin of its (Lp+1)-th value; the buffer keeps the bins up to it (only those
+//     below it when that would be more than the limit) and tau drops to the smallest
+//     value left out (every kept value is below it: the bin is monotone in the value);
 //   * a buffer that would overflow drops the values and records the smallest, which
 //     caps tau at the next refresh, so the first point holds again;
 //   * after the last tile a final refresh keeps at most KNN_OUT entries; four threads
@@ -1386,6 +1386,11 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
     }
     if (tid < 2)
         sm.need[tid] = 0u;
+    // every buffer slot starts at +inf (thread t: slots 32(t%4) .. +31 of query t/4)
+#pragma unroll
+    for (int i4 = 0; i4 < 8; ++i4)
+        *reinterpret_cast<float4 *>(&sm.bval[tid >> 2][32 * (tid & 3) + 4 * i4]) =
+            make_float4(INFINITY, INFINITY, INFINITY, INFINITY);
 
     const int lr0 = tid >> 3;
     const int c4 = (tid & 7) * 4;
@@ -1444,15 +1449,22 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
 
     // Refresh of every query's buffer (block-uniform call; four threads per query, one
     // quad of a wave, read and write its row, so no block barrier is needed; thread p
-    // holds entries 32p .. 32p+31).  fin: the final one (at most KNN_OUT kept).  The
-    // (Lp+1)-th live value is located by a 64-bin key K = min(floor(t * 64), 63),
-    // t = (v - min) / (max - min), monotone in v: 8 bins of K/8 with byte counters in
-    // registers summed over the quad, then the 8 sub-bins K%8 of the bin that holds it.
+    // holds slots 32p .. 32p+31).  Slots at or past a buffer's fill hold +inf (set at the
+    // item's start and rewritten by every compaction), so the live entries are the values
+    // below T0 = min(tau, lost).  fin: the final one (at most KNN_OUT kept).  The
+    // (Lp+1)-th live value is located on the scale t = (v - min) * sc, sc = 64 (1 - 2^-16)
+    // / (top - min), monotone in v and below 64 for every live value: byte counters of
+    // the 8 bins floor(t / 8) in one 64-bit register per thread, summed over the quad;
+    // then those of the 8 sub-bins floor(t) of the bin that holds it; and, when that
+    // sub-bin alone would take the buffer past its limit, those of its 8 parts floor(8t)
+    // (8t is exactly 8 times t, so the three levels nest).  The buffer keeps the parts up
+    // to the one that holds the (Lp+1)-th value (only those below it when that would be
+    // more than the limit) and tau drops to the smallest live value left out.
     auto refresh = [&](bool fin) __attribute__((always_inline)) {
         const int q = tid >> 2, p = tid & 3;
-        const bool qv = (uint32_t)q < qcnt;
         const uint32_t f = min(sm.fill[q], (uint32_t)KNN_CAP);
-        const float T0 = fminf(sm.tau[q], ord_val(sm.lost[q]));
+        const float tq = sm.tau[q];
+        const float T0 = fminf(tq, ord_val(sm.lost[q]));
         float v[32];
         uint32_t ip[16];
 #pragma unroll
@@ -1471,15 +1483,14 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
             ip[4 * i8 + 2] = w.z;
             ip[4 * i8 + 3] = w.w;
         }
-        // live entries: written (below the fill) and below T0; the others become +inf
+        // live entries: below T0 (the others become +inf)
         uint32_t n_own = 0u;
         float mn = INFINITY;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const bool l = qv && (uint32_t)(32 * p + i) < f && v[i] < T0;
-            v[i] = l ? v[i] : INFINITY;
-            n_own += l ? 1u : 0u;
-            mn = v[i] < mn ? v[i] : mn;
+            v[i] = v[i] < T0 ? v[i] : INFINITY;
+            n_own += v[i] < INFINITY ? 1u : 0u;
+            mn = fminf(mn, v[i]);
         }
         const uint32_t n_live = quad_sum(n_own);
         mn = quad_min(mn);
@@ -1496,88 +1507,127 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
         const uint32_t target = Lp + 1u;
         const uint32_t limit = fin ? KNN_OUT : KNN_KEEP;
         const bool hist = fin ? n_live > KNN_OUT : n_live > target;
-        // keys (s8 = 8 * s1 exactly, so K / 8 is the 8-bin index of t), four bytes a word
-        const float s1 = mx > mn ? 8.0f / (mx - mn) : 0.0f;
-        const float s8 = s1 * 8.0f;
+        // a row is rewritten when it is cut, holds dead slots below its fill, or a dropped
+        // value lowers its threshold; a wave with none of these leaves its rows as they are
+        if (__ballot(hist || n_live < f || T0 < tq) == 0)
+            return;
+        // keys floor(t) (dead slots: 127), four bytes a word
+        const float sc = mx > mn ? (64.0f * (1.0f - 0x1p-16f)) / (mx - mn) : 0.0f;
         uint32_t kw[8];
 #pragma unroll
         for (int w = 0; w < 8; ++w)
             kw[w] = 0u;
 #pragma unroll
         for (int i = 0; i < 32; ++i)
-            kw[i >> 2] |= min((uint32_t)((v[i] - mn) * s8), 63u) << ((i & 3) << 3);
+            kw[i >> 2] |= (uint32_t)fminf((v[i] - mn) * sc, 127.0f) << ((i & 3) << 3);
         auto key = [&](int i) { return (kw[i >> 2] >> ((i & 3) << 3)) & 0xFFu; };
-        // kept: the live entries with a key below kkey (every live entry without a
-        // histogram); kkey: past the key of the target-th value, or that key itself when
-        // keeping its bin would be more than the limit
-        uint32_t kkey = 64u;
-        if (hist) {
-            // byte b&3 of c[b>>2]: live entries with K/8 = b (at most 128: no carries)
-            uint32_t c0 = 0u, c1 = 0u;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const uint32_t k = key(i);
-                const uint32_t inc = v[i] < INFINITY ? 1u << (((k >> 3) & 3u) << 3) : 0u;
-                c0 += k < 32u ? inc : 0u;
-                c1 += k < 32u ? 0u : inc;
-            }
-            c0 = quad_sum(c0);
-            c1 = quad_sum(c1);
-            uint32_t cum = 0u, b1 = 0u, c_lt = 0u;
+        // the first of 8 counts (bytes of w0, w1) whose running sum from `below` reaches
+        // the target: its index, the running sum before it and the count itself
+        auto find_bin = [&](uint32_t w0, uint32_t w1, uint32_t below, uint32_t &bin, uint32_t &lt,
+                            uint32_t &cnt) __attribute__((always_inline)) {
+            uint32_t cum = below;
             bool found = false;
+            bin = 0u;
+            lt = below;
+            cnt = 0u;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const uint32_t c = ((b < 4 ? c0 : c1) >> ((b & 3) << 3)) & 0xFFu;
+                const uint32_t c = ((b < 4 ? w0 : w1) >> ((b & 3) << 3)) & 0xFFu;
                 const bool hit = !found && cum + c >= target;
-                b1 = hit ? (uint32_t)b : b1;
-                c_lt = hit ? cum : c_lt;
+                bin = hit ? (uint32_t)b : bin;
+                lt = hit ? cum : lt;
+                cnt = hit ? c : cnt;
                 found = found || hit;
                 cum += c;
             }
-            uint32_t d0 = 0u, d1 = 0u;
+        };
+        // kept: the keys below kkey (every live entry without a cut: live keys are <= 63);
+        // kkey: past the part that holds the target-th value, or that part itself when
+        // keeping it would be more than the limit
+        uint32_t kkey = 127u;
+        bool deep = false; // the target's sub-bin is crowded: the third level decides
+        uint32_t base3 = 0u, c_lt2 = 0u, c_le = 0u;
+        if (hist) {
+            // byte b of the 64-bit counter: entries with floor(t / 8) = b (at most 128: no
+            // carries); bin 7 also took the dead slots
+            uint64_t c8 = 0u;
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
-                const uint32_t k = key(i);
-                const uint32_t inc = (v[i] < INFINITY && (k >> 3) == b1) ? 1u << ((k & 3u) << 3) : 0u;
-                d0 += (k & 4u) ? 0u : inc;
-                d1 += (k & 4u) ? inc : 0u;
+                c8 += (uint64_t)1u << (key(i) & 0x38u);
+                asm("" : "+v"(c8)); // one running sum (no tree of 64-bit partial sums)
             }
-            d0 = quad_sum(d0);
-            d1 = quad_sum(d1);
-            uint32_t cum2 = c_lt, b2 = 0u, c_le = 0u;
-            found = false;
+            const uint32_t cw0 = quad_sum((uint32_t)c8);
+            const uint32_t cw1 = quad_sum((uint32_t)(c8 >> 32)) - ((128u - n_live) << 24);
+            uint32_t b1, c_lt, c_in;
+            find_bin(cw0, cw1, 0u, b1, c_lt, c_in);
+            // sub-bins floor(t) - 8 b1: entries below the bin count in sub-bin 0, those above
+            // it (and the dead slots) in sub-bin 7, taken out after the sums
+            uint64_t d8 = 0u;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                const uint32_t c = ((b < 4 ? d0 : d1) >> ((b & 3) << 3)) & 0xFFu;
-                const bool hit = !found && cum2 + c >= target;
-                b2 = hit ? (uint32_t)b : b2;
-                c_le = hit ? cum2 + c : c_le;
-                found = found || hit;
-                cum2 += c;
+            for (int i = 0; i < 32; ++i) {
+                const int sb = min(max((int)key(i) - (int)(8u * b1), 0), 7);
+                d8 += (uint64_t)1u << ((uint32_t)sb << 3);
+                asm("" : "+v"(d8));
             }
+            const uint32_t dw0 = quad_sum((uint32_t)d8) - c_lt;
+            const uint32_t dw1 = quad_sum((uint32_t)(d8 >> 32)) - ((128u - c_lt - c_in) << 24);
+            uint32_t b2, c_in2;
+            find_bin(dw0, dw1, c_lt, b2, c_lt2, c_in2);
+            c_le = c_lt2 + c_in2;
             kkey = 8u * b1 + b2 + (c_le <= limit ? 1u : 0u);
+            deep = c_le > limit;
+            base3 = 8u * (8u * b1 + b2);
+        }
+        if (__ballot(deep)) {
+            if (deep) {
+                // the 8 parts floor(8t) - base3 of the crowded sub-bin (8t is exactly 8 times
+                // t, so floor(8t) / 8 = floor(t)); the keys become 0 below it, 1 + the part
+                // inside it and 9 above it (dead slots stay 127)
+                const float sc8 = sc * 8.0f;
+                uint64_t e8 = 0u;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int r3 = (int)(uint32_t)fminf((v[i] - mn) * sc8, 1023.0f) - (int)base3;
+                    e8 += (uint64_t)1u << ((uint32_t)min(max(r3, 0), 7) << 3);
+                    asm("" : "+v"(e8));
+                    const uint32_t k3 = key(i) == 127u ? 127u : (uint32_t)min(max(r3 + 1, 0), 9);
+                    const int sh = (i & 3) << 3;
+                    kw[i >> 2] = (kw[i >> 2] & ~(0xFFu << sh)) | (k3 << sh);
+                }
+                const uint32_t ew0 = quad_sum((uint32_t)e8) - c_lt2;
+                const uint32_t ew1 = quad_sum((uint32_t)(e8 >> 32)) - ((128u - c_le) << 24);
+                uint32_t b3, c_lt3, c_in3;
+                find_bin(ew0, ew1, c_lt2, b3, c_lt3, c_in3);
+                kkey = 1u + b3 + (c_lt3 + c_in3 <= limit ? 1u : 0u);
+            }
         }
         // compaction to the front of the row (the entries are all in registers); tau
         // drops to the smallest live value left out (every kept value is below it)
         uint32_t nk_ = 0u;
-        bool kp[32];
         float tmin = INFINITY;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            kp[i] = v[i] < INFINITY && key(i) < kkey;
-            nk_ += kp[i] ? 1u : 0u;
-            tmin = (v[i] < INFINITY && !kp[i] && v[i] < tmin) ? v[i] : tmin;
+            const bool kp = key(i) < kkey;
+            nk_ += kp ? 1u : 0u;
+            tmin = kp ? tmin : fminf(tmin, v[i]);
         }
         const float tnew = hist ? fminf(T0, quad_min(tmin)) : T0;
         const uint32_t kincl = quad_incl(nk_, p);
         uint32_t pos = kincl - nk_;
+        // the row's slots become +inf, then the kept entries go to its front (the quad's
+        // LDS accesses execute in program order)
+#pragma unroll
+        for (int i4 = 0; i4 < 8; ++i4)
+            *reinterpret_cast<float4 *>(&sm.bval[q][32 * p + 4 * i4]) =
+                make_float4(INFINITY, INFINITY, INFINITY, INFINITY);
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            if (kp[i]) {
+            const bool kp = key(i) < kkey;
+            if (kp) {
                 sm.bval[q][pos] = v[i];
                 sm.bidx[q][pos] = (uint16_t)(ip[i >> 1] >> ((i & 1) << 4));
             }
-            pos += kp[i] ? 1u : 0u;
+            pos += kp ? 1u : 0u;
         }
         if (p == 3) {
             sm.fill[q] = kincl;
