@@ -894,25 +894,6 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
             // not be among the query's LT best (one queue already holds LT better ones),
             // and thresholds only decrease, so a stale value is safe.
             //
-            // The row's -|x|^2/2 is added by one more MFMA per accumulator: the A row
-            // carries it split exactly into three bf16 terms (k = 0..2, lane half 0; a
-            // padding row's -inf in the first term alone), B is 1 there and 0 elsewhere.
-            // The three products sum exactly to the fp32 value, so the MFMA performs the
-            // one rounded fp32 addition acc + (-|x|^2/2).
-            {
-                const bf16x8 bone = __builtin_bit_cast(
-                    bf16x8, make_uint4(h == 0 ? 0x3F803F80u : 0u, h == 0 ? 0x00003F80u : 0u, 0u, 0u));
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    const uint2 w = sm.nhx[slot][wm * 64 + 32 * mb + r];
-                    const bf16x8 abias =
-                        __builtin_bit_cast(bf16x8, make_uint4(h == 0 ? w.x : 0u, h == 0 ? w.y : 0u, 0u, 0u));
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bone, acc[mb][nb], 0, 0, 0);
-                }
-            }
-            //
             // Queues of LT = 8 and LT >= 16 also apply a counting bound, valid for any k:
             // the query's four queues hold m4 entries each at or below the largest of their
             // m4-th entries (4*m4 >= Lp+1 entries in all), so a candidate at or above that
@@ -948,20 +929,77 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                 tsh[nb] = t;
                 ncth[nb] = -s_bound(t, qnv[nb]);
             }
+            // The row's -|x|^2/2 and the pre-filter bound are added by one more MFMA per
+            // accumulator: the A row carries -|x|^2/2 split exactly into three bf16 terms
+            // (k = 0..2, lane half 0; a padding row's -inf in the first term alone) and 1 at
+            // k = 3..5; B is 1 at k = 0..2 and carries the query column's bound cb split
+            // exactly into three bf16 terms (truncations: hi + mid + lo = cb) at k = 3..5.
+            // So acc = -s + cb and a candidate is pending iff acc > 0 (s < cb; the sign
+            // bit, a padding row's -inf included, rejects it), and the round reads
+            // -s = acc - cb.  cb (s-space, with slack: a superset of a < tsh) is the larger
+            // of the column's two lanes' bounds; it is 0 on the first tile and whenever
+            // some lane of the wave has no finite bound yet (then the pending test is
+            // -cb' - acc < 0 with the lane's own bound cb', as before the fold).
+            float cb[NB];
+            bool fold = tile > 0;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                cb[nb] = fmaxf(-ncth[nb], -__shfl_xor(ncth[nb], 32));
+                fold = fold && cb[nb] < INFINITY;
+            }
+            fold = __ballot(!fold) == 0;
+            {
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    cb[nb] = fold ? cb[nb] : 0.0f;
+                bf16x8 bcol[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t u0 = __float_as_uint(cb[nb]) & 0xFFFF0000u;
+                    const float r1 = cb[nb] - __uint_as_float(u0);
+                    const uint32_t u1 = __float_as_uint(r1) & 0xFFFF0000u;
+                    const uint32_t u2 = __float_as_uint(r1 - __uint_as_float(u1)) & 0xFFFF0000u;
+                    // k = 0..7 (lane half 1 meets zeros in A): 1, 1, 1, hi, mid, lo, 0, 0
+                    bcol[nb] = __builtin_bit_cast(bf16x8, make_uint4(0x3F803F80u, 0x3F80u | u0, (u1 >> 16) | u2, 0u));
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb) {
+                    const uint2 w = sm.nhx[slot][wm * 64 + 32 * mb + r];
+                    const bf16x8 abias = __builtin_bit_cast(
+                        bf16x8, make_uint4(h == 0 ? w.x : 0u, h == 0 ? (w.y | 0x3F800000u) : 0u, h == 0 ? 0x3F803F80u : 0u, 0u));
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(abias, bcol[nb], acc[mb][nb], 0, 0, 0);
+                }
+            }
             // branch-free pass: per list a lane mask whose bit (31 - j) marks element j
-            // under the pre-filter bound (s < c  <=>  the sign bit of -c - acc; a NaN
-            // from -inf - -inf only marks a padding row, which the round rejects)
+            // under the pre-filter bound (folded: the sign bit of acc, inverted; otherwise
+            // s < c  <=>  the sign bit of -c - acc, where a NaN from -inf - -inf only marks a
+            // padding row, which the round rejects)
             uint32_t pend[NB];
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 pend[nb] = 0u;
+            if (fold) {
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+                for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
+                    for (int i = 0; i < 16; ++i)
 #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-                        pend[nb] = (pend[nb] << 1) | (__float_as_uint(ncth[nb] - acc[mb][nb][i]) >> 31);
+                        for (int nb = 0; nb < NB; ++nb)
+                            pend[nb] = (pend[nb] << 1) | (__float_as_uint(acc[mb][nb][i]) >> 31);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    pend[nb] = ~pend[nb];
+            } else {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+                            pend[nb] = (pend[nb] << 1) | (__float_as_uint(ncth[nb] - acc[mb][nb][i]) >> 31);
+            }
             // self exclusion (candidate space = query space): clear the query's own bit
             uint32_t self_j[NB];
 #pragma unroll
@@ -996,7 +1034,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
                     const uint32_t j = (uint32_t)__builtin_clz(m | 1u);
                     const bool act = m != 0u;
                     m &= ~(0x80000000u >> j);
-                    const float av = staged(j);
+                    const float av = staged(j) - cb[nb];
                     const uint32_t rid = sm.rowid[slot][tile_row(wm, h, j)];
                     float dd = __builtin_fmaf(-2.0f, av, qnv[nb]);
                     dd = (act && dd < ld[nb][LT - 1] && dd < tsh[nb]) ? dd : INFINITY;
@@ -1005,7 +1043,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
             };
             // (dist, id) of element j of list nb for the first tile's sorting network
             auto entry = [&](int nb, int j, uint32_t idg, float &dd, uint32_t &id) __attribute__((always_inline)) {
-                dd = __builtin_fmaf(-2.0f, acc[j >> 4][nb][j & 15], qnv[nb]);
+                dd = __builtin_fmaf(-2.0f, acc[j >> 4][nb][j & 15] - cb[nb], qnv[nb]);
                 if constexpr (EXCL)
                     dd = (uint32_t)j == self_j[nb] ? INFINITY : dd;
                 id = dd < INFINITY ? idg : NONE;

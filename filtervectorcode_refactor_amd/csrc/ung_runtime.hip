@@ -488,16 +488,18 @@ int launch_knn_select(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &
 //    truncates each of its 17 operands by at most one ulp of the largest and rounds once
 //    gives <= 17u per MFMA over 3d/16 MFMAs, 3.19 d*u*1.0079 |x||q|.  In a: <= 1.61 d*u
 //    (|q|+R)^2
-//  * adding -fl(|x|^2)/2 by one more MFMA whose three bf16 products sum exactly to that
-//    fp32 value: one rounding (measured), at most 4 operand truncations and one rounding
-//    in the fused-adder model above, <= 4.5 u max(|acc|, |x|^2/2) <= 2.25 u (|q|+R)^2;
-//    the final fma: <= 1.01 u (|q|+R)^2
-// Sum <= (1.61 d + 100.6) u (|q|+R)^2; the factor below keeps a margin.  Flushed bf16 or
+//  * adding -fl(|x|^2)/2 and the pre-filter bound cb (|cb| <= (|q|+R)^2: a threshold
+//    distance at most (|q|+R)^2, halved, plus |q|^2/2) by one more MFMA whose six bf16
+//    products sum exactly to those two fp32 values: at most 7 operand truncations and one
+//    rounding in the fused-adder model above, <= 7.5 u max(|acc|, |x|^2/2, |cb|) <=
+//    7.5 u (|q|+R)^2, then -s read back as fl(acc - cb): <= 2 u (|q|+R)^2, so in a:
+//    <= 19 u (|q|+R)^2; the final fma: <= 1.01 u (|q|+R)^2
+// Sum <= (1.61 d + 117.4) u (|q|+R)^2; the factor below keeps a margin.  Flushed bf16 or
 // fp32 subnormals add at most ~6d * 2^-126 absolute, covered by the 1e-30 term of
 // lower_bound_exact.
 double eps_coef_for(uint32_t d)
 {
-    return (1.75 * (double)d + 112.0) * std::ldexp(1.0, -24);
+    return (1.75 * (double)d + 132.0) * std::ldexp(1.0, -24);
 }
 
 // PlanMem in the workspace's own buffers, grown to the plan (hipMalloc / hipHostMalloc
