@@ -248,18 +248,24 @@ __device__ __forceinline__ void list_insert(float (&ld)[LT], uint32_t (&li)[LT],
     li[0] = c_hi ? ni : li[0];
 }
 
-// Lower bound on the exact (reference-rounded) distance of any candidate whose
-// expansion-form MFMA distance is >= A:
+// Error term of one query, computed once per row: ea = eps_coef * (|q| + R)^2 (|q| from
+// the cached |q|^2, rounded up), with
 //   |a - D| <= eps_coef * (|q| + R)^2   (norm cache, MFMA dot, epilogue roundings)
-//   e >= D * (1 - shrink)               (reference summation)
-// Rounded toward -inf when narrowed to fp32.
-__device__ __forceinline__ float lower_bound_exact(float A, float qn, double eps_coef, double shrink, double rmax)
+//   e >= D * (1 - shrink), e <= D * (1 + shrink)   (reference summation)
+// for the expansion-form MFMA value a, the exact squared distance D and the reference's
+// rounded value e.
+__device__ __forceinline__ double bound_ea(float qn, double eps_coef, double rmax)
+{
+    const double r = sqrt((double)fmaxf(qn, 0.0f) * (1.0 + 1e-6)) + rmax;
+    return eps_coef * r * r;
+}
+
+// Lower bound on the exact (reference-rounded) distance of any candidate whose
+// expansion-form MFMA distance is >= A, rounded toward -inf when narrowed to fp32.
+__device__ __forceinline__ float lower_bound_ea(float A, double ea, double shrink)
 {
     if (!(A < INFINITY))
         return INFINITY;
-    const double qnorm = sqrt((double)fmaxf(qn, 0.0f) * (1.0 + 1e-6));
-    const double r = qnorm + rmax;
-    const double ea = eps_coef * r * r;
     double b = ((double)A - ea);
     b = b > 0.0 ? b * (1.0 - shrink) : b * (1.0 + shrink);
     b -= 1e-30;
@@ -268,16 +274,31 @@ __device__ __forceinline__ float lower_bound_exact(float A, float qn, double eps
 
 // Upper bound on the exact (reference-rounded) distance of a candidate whose
 // expansion-form MFMA distance is A (the same two error terms, the other way; the
-// exact distance is >= 0).  Rounded toward +inf.
-__device__ __forceinline__ float upper_bound_exact(float A, float qn, double eps_coef, double shrink, double rmax)
+// exact distance is >= 0), rounded toward +inf.
+__device__ __forceinline__ float upper_bound_ea(float A, double ea, double shrink)
 {
     if (!(A < INFINITY))
         return INFINITY;
-    const double qnorm = sqrt((double)fmaxf(qn, 0.0f) * (1.0 + 1e-6));
-    const double r = qnorm + rmax;
-    const double ea = eps_coef * r * r;
     const double b = fmax((double)A + ea, 0.0) * (1.0 + shrink) + 1e-30;
     return __double2float_ru(b);
+}
+
+// (dist, id) ascending sort of one value per lane over the wave (bitonic network, 21
+// exchange stages): lane t ends with the t-th smallest.
+__device__ __forceinline__ void wave_sort64(float &d, uint32_t &id, int lane)
+{
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const float od = __shfl_xor(d, j);
+            const uint32_t oi = __shfl_xor(id, j);
+            const bool up = (lane & k) == 0;
+            const bool lower = (lane & j) == 0;
+            const bool take = (lower == up) ? cand_less(od, oi, d, id) : cand_less(d, id, od, oi);
+            d = take ? od : d;
+            id = take ? oi : id;
+        }
 }
 
 // (dist, id) argmin across the wave; every lane ends with the minimum.
@@ -1947,6 +1968,30 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
                 ca[h] = M.part_dist[prow * Lp + 64 * h + lane];
             }
         B = M.part_bound[prow];
+    } else if (S * Lp <= 64u) {
+        // all S*Lp entries in the wave (one per lane; splits are disjoint, so the ids of the
+        // entries are distinct, NONE aside): a wave sort by (dist, id) puts the entry of
+        // rank t in lane t, the one of rank Lp is the first left out
+        const uint32_t n = S * Lp;
+        float ed = INFINITY;
+        uint32_t eid = NONE;
+        if ((uint32_t)lane < n) {
+            const uint32_t sp = (uint32_t)lane / Lp, pos = (uint32_t)lane - sp * Lp;
+            const size_t prow = (size_t)jb.part_base + (size_t)sp * jb.q_count + ql;
+            ed = M.part_dist[prow * Lp + pos];
+            eid = M.part_ids[prow * Lp + pos];
+        }
+        float bnd = (uint32_t)lane < S ? M.part_bound[(size_t)jb.part_base + (size_t)lane * jb.q_count + ql] : INFINITY;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            bnd = fminf(bnd, __shfl_xor(bnd, off));
+        wave_sort64(ed, eid, lane);
+        if ((uint32_t)lane < Lp) {
+            ci[0] = eid;
+            ca[0] = ed;
+        }
+        const float a_next = __shfl(ed, (int)Lp); // Lp < 64 here
+        B = fminf(bnd, a_next);
     } else if (S * Lp <= 128u) {
         // all S*Lp entries in the wave (two per lane): each entry's rank under (dist, id,
         // entry index) by comparing with every other one, no dependent loads; the entry of
@@ -2064,23 +2109,26 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
     }
 
     // Only candidates that can be among the k best are re-scored: the k best by
-    // approximate distance all have exact distances <= U = upper_bound_exact(a_{k-1}), so
+    // approximate distance all have exact distances <= U = upper_bound_ea(a_{k-1}), so
     // the k-th exact distance T <= U, and a candidate whose lower bound exceeds U has an
     // exact distance > T (it is neither a result nor needed by the certificate).  The
     // candidates are in ascending approximate order, so the re-scored ones are a prefix.
     const float xq = M.xn[q];
+    const double ea = bound_ea(xq, M.eps_coef, M.rmax);
     uint32_t m_need = Lp;
     if (k <= Lp) {
         const int src = (int)((k - 1u) & 63u);
         const float ak = k - 1u < 64u ? __shfl(ca[0], src) : __shfl(ca[1], src);
-        const float U = upper_bound_exact(ak, xq, M.eps_coef, M.shrink, M.rmax);
+        const float U = upper_bound_ea(ak, ea, M.shrink);
         if (U < INFINITY) {
             uint32_t cnt_need = 0;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const bool in = (uint32_t)(64 * h + lane) < Lp;
-                const bool need = in && !(lower_bound_exact(ca[h], xq, M.eps_coef, M.shrink, M.rmax) > U);
-                cnt_need += (uint32_t)__popcll(__ballot(need));
+                if (64u * (uint32_t)h < Lp) {
+                    const bool in = (uint32_t)(64 * h + lane) < Lp;
+                    const bool need = in && !(lower_bound_ea(ca[h], ea, M.shrink) > U);
+                    cnt_need += (uint32_t)__popcll(__ballot(need));
+                }
             }
             m_need = cnt_need;
         }
@@ -2113,6 +2161,36 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
             }
         }
     }
+    const size_t orow = (size_t)jb.out_row + ql;
+    const float Bx = lower_bound_ea(B, ea, M.shrink);
+    if (m_need <= 64u && m_need > 16u) {
+        // one candidate per lane: a wave sort by (exact, id) puts rank t in lane t (the
+        // re-scored ids are distinct; left-out lanes hold (+inf, NONE) and sort last).
+        // Its 21 exchange stages cost less than the rank loop below from about 16
+        // candidates on.
+        const bool real = (uint32_t)lane < m_need && ci[0] != NONE;
+        float d = real ? ex[0] : INFINITY;
+        uint32_t id = real ? ci[0] : NONE;
+        wave_sort64(d, id, lane);
+        const float T = __shfl(d, (int)(k - 1u)); // k <= 64
+        const uint32_t cnt = (uint32_t)__popcll(__ballot((uint32_t)lane < k && id != NONE));
+        const bool certified = (cnt < k) ? !(B < INFINITY) : (T < Bx);
+        if (!certified) {
+            if (lane == 0) {
+                const uint32_t slot = atomicAdd(M.flag_count, 1u);
+                M.flagged[slot] = make_uint2(mi.job, ql);
+            }
+            return;
+        }
+        if ((uint32_t)lane < k) {
+            M.out_ids[orow * k + lane] = id != NONE ? id - jb.id_base : NONE;
+            if (M.out_dist)
+                M.out_dist[orow * k + lane] = id != NONE ? d : INFINITY;
+        }
+        if (lane == 0 && M.out_size)
+            M.out_size[orow] = (int32_t)cnt;
+        return;
+    }
     // rank under (exact, id, position); a left-out candidate (exact distance > T) ranks
     // after every re-scored one and takes no place in the row
     uint32_t rank[2] = {0u, 0u};
@@ -2139,7 +2217,6 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
         T = fminf(T, __shfl_xor(T, off));
-    const float Bx = lower_bound_exact(B, xq, M.eps_coef, M.shrink, M.rmax);
     const bool certified = (cnt < k) ? !(B < INFINITY) : (T < Bx);
     if (!certified) {
         if (lane == 0) {
@@ -2148,7 +2225,6 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
         }
         return;
     }
-    const size_t orow = (size_t)jb.out_row + ql;
 #pragma unroll
     for (int h = 0; h < 2; ++h)
         if (mine[h] && rank[h] < k) {
@@ -2748,23 +2824,6 @@ __global__ __launch_bounds__(256) void ung_reverse_kernel(PruneParams K)
             }
         }
     }
-}
-
-// (dist, id) ascending sort of one value per lane over the wave.
-__device__ __forceinline__ void wave_sort64(float &d, uint32_t &id, int lane)
-{
-#pragma unroll
-    for (int k = 2; k <= 64; k <<= 1)
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            const float od = __shfl_xor(d, j);
-            const uint32_t oi = __shfl_xor(id, j);
-            const bool up = (lane & k) == 0;
-            const bool lower = (lane & j) == 0;
-            const bool take = (lower == up) ? cand_less(od, oi, d, id) : cand_less(d, id, od, oi);
-            d = take ? od : d;
-            id = take ? oi : id;
-        }
 }
 
 // One wave (block) per row: forward candidates + the reverse_cap nearest reverse edges,

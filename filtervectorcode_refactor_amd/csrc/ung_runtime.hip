@@ -496,7 +496,7 @@ int launch_knn_select(ung_hip_ctx *ctx, hipStream_t stream, const SelectParams &
 //    <= 19 u (|q|+R)^2; the final fma: <= 1.01 u (|q|+R)^2
 // Sum <= (1.61 d + 117.4) u (|q|+R)^2; the factor below keeps a margin.  Flushed bf16 or
 // fp32 subnormals add at most ~6d * 2^-126 absolute, covered by the 1e-30 term of
-// lower_bound_exact.
+// lower_bound_ea.
 double eps_coef_for(uint32_t d)
 {
     return (1.75 * (double)d + 132.0) * std::ldexp(1.0, -24);
