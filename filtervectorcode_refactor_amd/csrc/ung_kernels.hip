@@ -2521,18 +2521,25 @@ __global__ void ung_addl_mark_kernel(const uint32_t *__restrict__ ids, uint32_t 
 // (src/uni_nav_graph_cross_edges.cpp:543-562: vectors of C in order, per edges each, until
 // num_cross are appended); 0 for reached entries and for entries of no group (eg = 0).
 // cnt[0] += scored (query, candidate) pairs, cnt[1] += entries that add edges.
+// Additional edges: a target group of more than ADDL_SMALL vectors is scanned in ranges of
+// ADDL_RANGE, one wave each (a query row of a large group spreads over many waves).
+constexpr uint32_t ADDL_SMALL = 8;     // target groups up to this size: one thread per entry
+constexpr uint32_t ADDL_RANGE = 1024;  // candidates per scan item
+
 __global__ void ung_addl_count_kernel(const uint32_t *__restrict__ gb, const uint32_t *__restrict__ oi,
                                       const uint32_t *__restrict__ eg, const uint32_t *__restrict__ reached,
                                       uint32_t E, uint32_t num_cross, uint32_t *__restrict__ rows,
-                                      uint32_t *__restrict__ edges, unsigned long long *__restrict__ cnt)
+                                      uint32_t *__restrict__ edges, uint32_t *__restrict__ items,
+                                      unsigned long long *__restrict__ cnt)
 {
     unsigned long long my_pairs = 0, my_entries = 0;
     for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < E; p += gridDim.x * blockDim.x) {
-        uint32_t m = 0, per = 0;
+        uint32_t m = 0, per = 0, nx = 0;
         const uint32_t c = eg[p];
         if (!reached[p] && c != 0) {
             const uint32_t x = oi[p];
-            const uint32_t nc = gb[c + 1] - gb[c], nx = gb[x + 1] - gb[x];
+            const uint32_t nc = gb[c + 1] - gb[c];
+            nx = gb[x + 1] - gb[x];
             per = min(nx, num_cross / 2u);
             if (per > 0 && nc > 0)
                 m = min(nc, (num_cross + per - 1) / per);
@@ -2541,6 +2548,7 @@ __global__ void ung_addl_count_kernel(const uint32_t *__restrict__ gb, const uin
         }
         rows[p] = m;
         edges[p] = m * per;
+        items[p] = nx > ADDL_SMALL ? m * ((nx + ADDL_RANGE - 1) / ADDL_RANGE) : 0u;
     }
     if (my_pairs)
         atomicAdd(&cnt[0], my_pairs);
@@ -2548,47 +2556,136 @@ __global__ void ung_addl_count_kernel(const uint32_t *__restrict__ gb, const uin
         atomicAdd(&cnt[1], my_entries);
 }
 
-// Additional edges, step 3: one wave per LNG entry p = (C, X) with a target group of more
-// than ADDL_SMALL vectors, for each of its query rows j (vector j of C): an exact scan of
-// X's range in the reference's summation order and (dist, id) order, the first `per`
-// results written to their final place in the per-group edge lists (entries in LNG order,
-// vectors, ranks).
+// Additional edges, step 3: scan items (an entry p = (C, X) with a target group of more
+// than ADDL_SMALL vectors has m query rows, vectors 0..m-1 of C, times ceil(|X| /
+// ADDL_RANGE) ranges of X): one wave per item scans its range in the reference's summation
+// order and keeps the first `per` by (dist, id).  A row of one range writes its results to
+// their final place in the per-group edge lists (entries in LNG order, vectors, ranks);
+// the ranges of a larger row write partial lists that ung_addl_merge_kernel merges.
 struct AddlParams {
     const float *X;
     uint32_t d;
     const uint32_t *gb, *oi, *eg;
     const uint32_t *row_off, *edge_off; // [E+1] exclusive scans
-    uint32_t E;
+    const uint32_t *item_off;           // [E+1] exclusive scan of the scan items
+    const uint32_t *item_entry;         // [I] entry of each scan item
+    uint32_t E, I;
     uint32_t per_max;
+    uint32_t *part_ids; // [I x per_max] partial lists of the rows of several ranges
+    float *part_dist;
     uint32_t *from, *to;
 };
 
-constexpr uint32_t ADDL_SMALL = 8; // target groups up to this size: one thread per entry
+// The entry of each scan item (one thread per entry).
+__global__ void ung_addl_expand_kernel(const uint32_t *__restrict__ item_off, uint32_t E,
+                                       uint32_t *__restrict__ item_entry)
+{
+    for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < E; p += gridDim.x * blockDim.x)
+        for (uint32_t w = item_off[p]; w < item_off[p + 1]; ++w)
+            item_entry[w] = p;
+}
+
+// Where scan item w sits: its entry, target range, query row and ranges per row.
+struct AddlItem {
+    uint32_t p, q, x0, nx, nr, j, r, per;
+};
+__device__ __forceinline__ AddlItem addl_item(const AddlParams &A, uint32_t w)
+{
+    AddlItem t;
+    t.p = A.item_entry[w];
+    const uint32_t c = A.eg[t.p], x = A.oi[t.p];
+    t.x0 = A.gb[x];
+    t.nx = A.gb[x + 1] - t.x0;
+    t.nr = (t.nx + ADDL_RANGE - 1) / ADDL_RANGE;
+    const uint32_t loc = w - A.item_off[t.p];
+    t.j = loc / t.nr;
+    t.r = loc - t.j * t.nr;
+    t.q = A.gb[c] + t.j;
+    t.per = min(t.nx, A.per_max);
+    return t;
+}
 
 __global__ __launch_bounds__(64) void ung_addl_scan_kernel(AddlParams A)
 {
     __shared__ float sd[64][33];
     __shared__ uint32_t si[64][33];
     const int lane = threadIdx.x;
-    // one wave per LNG entry (grid-stride), its query rows one after the other; entries
-    // with no rows or a small target group are skipped (uniform: one wave per block)
-    for (uint32_t p = blockIdx.x; p < A.E; p += gridDim.x) {
-        const uint32_t m = A.row_off[p + 1] - A.row_off[p];
-        if (m == 0)
-            continue;
-        const uint32_t c = A.eg[p], x = A.oi[p];
-        const uint32_t x0 = A.gb[x], x1 = A.gb[x + 1];
-        if (x1 - x0 <= ADDL_SMALL)
-            continue; // ung_addl_small_kernel's entry
-        const uint32_t per = min(x1 - x0, A.per_max);
-        for (uint32_t j = 0; j < m; ++j) {
-            const uint32_t q = A.gb[c] + j;
-            const float *qv = A.X + (size_t)q * A.d;
-            int32_t size = 0;
-            for (uint32_t g = x0 + (uint32_t)lane; g < x1; g += 64) {
-                const float dist = l2_ref_lane(qv, A.X + (size_t)g * A.d, A.d);
+    for (uint32_t w = blockIdx.x; w < A.I; w += gridDim.x) {
+        const AddlItem t = addl_item(A, w);
+        const float *qv = A.X + (size_t)t.q * A.d;
+        const uint32_t v0 = t.x0 + t.r * ADDL_RANGE, v1 = min(t.x0 + t.nx, v0 + ADDL_RANGE);
+        const uint32_t per = t.per;
+        int32_t size = 0;
+        for (uint32_t g = v0 + (uint32_t)lane; g < v1; g += 64) {
+            const float dist = l2_ref_lane(qv, A.X + (size_t)g * A.d, A.d);
+            if (size == (int32_t)per && !cand_less(dist, g, sd[lane][size - 1], si[lane][size - 1]))
+                continue;
+            int32_t pos = size < (int32_t)per ? size : (int32_t)per - 1;
+            while (pos > 0 && cand_less(dist, g, sd[lane][pos - 1], si[lane][pos - 1])) {
+                sd[lane][pos] = sd[lane][pos - 1];
+                si[lane][pos] = si[lane][pos - 1];
+                --pos;
+            }
+            sd[lane][pos] = dist;
+            si[lane][pos] = g;
+            if (size < (int32_t)per)
+                ++size;
+        }
+        // per rounds of a (dist, id) argmin over the lane heads
+        int head = 0;
+        const size_t o = (size_t)A.edge_off[t.p] + (size_t)t.j * per;
+        for (uint32_t k = 0; k < per; ++k) {
+            const float hd = head < size ? sd[lane][head] : INFINITY;
+            const uint32_t hi2 = head < size ? si[lane][head] : NONE;
+            float bd = hd;
+            uint32_t bi = hi2;
+            for (int off = 32; off > 0; off >>= 1) {
+                const float od = __shfl_xor(bd, off);
+                const uint32_t oi2 = __shfl_xor(bi, off);
+                if (cand_less(od, oi2, bd, bi)) {
+                    bd = od;
+                    bi = oi2;
+                }
+            }
+            if (bi != NONE && hi2 == bi)
+                ++head;
+            if (lane == 0) {
+                if (t.nr == 1) {
+                    A.from[o + k] = t.q;
+                    A.to[o + k] = bi;
+                } else {
+                    A.part_ids[(size_t)w * A.per_max + k] = bi;
+                    A.part_dist[(size_t)w * A.per_max + k] = bd;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// The rows of several ranges (the item of range 0 stands for the row): lane l first keeps
+// the per best entries of ranges l, l+64, ... (each list sorted, ranges disjoint) in its
+// LDS queue, then per rounds of a (dist, id) argmin over the lane heads.
+__global__ __launch_bounds__(64) void ung_addl_merge_kernel(AddlParams A)
+{
+    __shared__ float sd[64][33];
+    __shared__ uint32_t si[64][33];
+    const int lane = threadIdx.x;
+    for (uint32_t w = blockIdx.x; w < A.I; w += gridDim.x) {
+        const AddlItem t = addl_item(A, w);
+        if (t.nr == 1 || t.r != 0)
+            continue; // uniform: one wave per block
+        const uint32_t per = t.per;
+        int32_t size = 0;
+        for (uint32_t rr = (uint32_t)lane; rr < t.nr; rr += 64) {
+            const size_t base = (size_t)(w + rr) * A.per_max;
+            for (uint32_t k = 0; k < per; ++k) {
+                const uint32_t g = A.part_ids[base + k];
+                if (g == NONE)
+                    break; // a range's list is sorted, NONE entries come last
+                const float dist = A.part_dist[base + k];
                 if (size == (int32_t)per && !cand_less(dist, g, sd[lane][size - 1], si[lane][size - 1]))
-                    continue;
+                    break; // the rest of this sorted list can not enter either
                 int32_t pos = size < (int32_t)per ? size : (int32_t)per - 1;
                 while (pos > 0 && cand_less(dist, g, sd[lane][pos - 1], si[lane][pos - 1])) {
                     sd[lane][pos] = sd[lane][pos - 1];
@@ -2600,30 +2697,30 @@ __global__ __launch_bounds__(64) void ung_addl_scan_kernel(AddlParams A)
                 if (size < (int32_t)per)
                     ++size;
             }
-            int head = 0;
-            const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
-            for (uint32_t t = 0; t < per; ++t) {
-                const float hd = head < size ? sd[lane][head] : INFINITY;
-                const uint32_t hi2 = head < size ? si[lane][head] : NONE;
-                float bd = hd;
-                uint32_t bi = hi2;
-                for (int off = 32; off > 0; off >>= 1) {
-                    const float od = __shfl_xor(bd, off);
-                    const uint32_t oi2 = __shfl_xor(bi, off);
-                    if (cand_less(od, oi2, bd, bi)) {
-                        bd = od;
-                        bi = oi2;
-                    }
-                }
-                if (bi != NONE && hi2 == bi)
-                    ++head;
-                if (lane == 0) {
-                    A.from[o + t] = q;
-                    A.to[o + t] = bi;
+        }
+        int head = 0;
+        const size_t o = (size_t)A.edge_off[t.p] + (size_t)t.j * per;
+        for (uint32_t k = 0; k < per; ++k) {
+            const float hd = head < size ? sd[lane][head] : INFINITY;
+            const uint32_t hi2 = head < size ? si[lane][head] : NONE;
+            float bd = hd;
+            uint32_t bi = hi2;
+            for (int off = 32; off > 0; off >>= 1) {
+                const float od = __shfl_xor(bd, off);
+                const uint32_t oi2 = __shfl_xor(bi, off);
+                if (cand_less(od, oi2, bd, bi)) {
+                    bd = od;
+                    bi = oi2;
                 }
             }
-            __syncthreads();
+            if (bi != NONE && hi2 == bi)
+                ++head;
+            if (lane == 0) {
+                A.from[o + k] = t.q;
+                A.to[o + k] = bi;
+            }
         }
+        __syncthreads();
     }
 }
 

@@ -191,7 +191,7 @@ struct PlanMem {
 struct Workspace {
     hipStream_t stream = nullptr;
     hipStream_t upload = nullptr; // merge-item uploads, beside the select kernel
-    hipEvent_t ev[4] = {};
+    hipEvent_t ev[5] = {};        // select start, select end, merge end, rescan end, merge start
     hipEvent_t ev_up = nullptr;   // merge items uploaded
     DevBuf<Job> jobs;
     DevBuf<Item> items;
@@ -272,6 +272,8 @@ struct ung_hip_ctx {
     // additional edges: group ranges, LNG rows, point groups, reached flags, entry groups,
     // per-entry row/edge counts (scanned in place), group offsets, edge lists, counters
     DevBuf<uint32_t> a_gb, a_op, a_oi, a_pg, a_reached, a_eg, a_rows, a_edges, a_ptr, a_from, a_to;
+    DevBuf<uint32_t> a_items, a_ientry, a_pid; // additional-edge scan items and their partial lists
+    DevBuf<float> a_pdist;
     DevBuf<unsigned long long> a_cnt;
     DevBuf<unsigned char> a_tmp;
     HostBuf a_stage;
@@ -618,6 +620,8 @@ void stage_plan(ung_hip_ctx *ctx, const Plan &pl, const StageLayout &L, char *hs
 // plan_launch uploads the work lists and enqueues the select and merge kernels;
 // plan_finish reads the flagged-row count back, rescans those rows and collects the
 // statistics.
+int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, PlanMem &m, ung_hip_stats *st);
+
 int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, PlanMem &m, ung_hip_stats *st,
                 hipEvent_t start_after = nullptr)
 {
@@ -680,13 +684,24 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     if (rc)
         return rc;
     HIPCHECK(hipEventRecord(ws.ev[1], ws.stream));
+    return plan_launch_merge(ctx, ws, pl, k, m, st);
+}
 
+// The merge of a launched plan, after its select kernel on ws.stream.
+int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, PlanMem &m, ung_hip_stats *st)
+{
+    if (pl.jobs.empty())
+        return UNG_HIP_OK;
+    const uint32_t lp = pick_lp(k, pick_lt(k));
+    const StageLayout L = stage_layout(pl);
+    char *hs = m.stage;
     // merge items, built and uploaded (on the upload stream) while the select kernel runs
     const auto t_mi = clk::now();
     write_merge_items(pl, reinterpret_cast<MergeItem *>(hs + L.om));
     HIPCHECK(hipMemcpyAsync(m.mitems, hs + L.om, L.bm, hipMemcpyHostToDevice, ws.upload));
     HIPCHECK(hipEventRecord(ws.ev_up, ws.upload));
     HIPCHECK(hipStreamWaitEvent(ws.stream, ws.ev_up, 0));
+    HIPCHECK(hipEventRecord(ws.ev[4], ws.stream));
     if (st)
         st->h2d_ms += ms_since(t_mi);
 
@@ -701,9 +716,9 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     M.part_bound = m.part_bound;
     M.lp = lp;
     M.k = k;
-    M.eps_coef = P.eps_coef;
-    M.shrink = P.shrink;
-    M.rmax = P.rmax;
+    M.eps_coef = eps_coef_for(ctx->d) * ctx->eps_scale;
+    M.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
+    M.rmax = ctx->rmax;
     M.out_ids = m.out_ids;
     M.out_dist = m.out_dist;
     M.out_size = m.out_size;
@@ -792,7 +807,7 @@ int plan_finish(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     if (st) {
         float a = 0, b = 0, c = 0;
         HIPCHECK(hipEventElapsedTime(&a, ws.ev[0], ws.ev[1]));
-        HIPCHECK(hipEventElapsedTime(&b, ws.ev[1], ws.ev[2]));
+        HIPCHECK(hipEventElapsedTime(&b, ws.ev[4], ws.ev[2]));
         HIPCHECK(hipEventElapsedTime(&c, ws.ev[2], ws.ev[3]));
         st->select_ms += a;
         st->merge_ms += b;
@@ -1119,8 +1134,10 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     if ((rc = build_group_plan(ctx, n_groups, grp_begin, grp_size, list_k, ctx->intra_plan)))
         return rc;
     ctx->intra_stats.plan_ms += ms_since(ctx->intra_t0);
-    // the group call's kernels start when the cross select ends: they fill the chip while
-    // the cross merge (memory-bound), rescan and the caller's next steps run
+    // the group call's kernels start when the cross select ends: they share the chip with
+    // the cross merge (bound by its re-score loads), the rescan and the caller's additional
+    // edges, whose different bounds fill each other's gaps (cfg2: 17.7 ms a step, against
+    // 18.0 ms with the group select alone between the cross merge and the additional edges)
     PlanMem m0;
     if ((rc = cross_prepare_result(ctx, k)) ||
         (rc = workspace_mem(ctx->ws[0], pl, pick_lp(k, pick_lt(k)), ctx->cross, m0)) ||
@@ -1366,7 +1383,8 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     // inputs through pinned staging
     if ((rc = ctx->a_gb.ensure(G + 2)) || (rc = ctx->a_op.ensure(G + 2)) || (rc = ctx->a_oi.ensure(E + 1)) ||
         (rc = ctx->a_pg.ensure(N)) || (rc = ctx->a_reached.ensure(E + 1)) || (rc = ctx->a_eg.ensure(E + 1)) ||
-        (rc = ctx->a_rows.ensure(E + 1)) || (rc = ctx->a_edges.ensure(E + 1)) || (rc = ctx->a_ptr.ensure(G + 2)) ||
+        (rc = ctx->a_rows.ensure(E + 1)) || (rc = ctx->a_edges.ensure(E + 1)) || (rc = ctx->a_items.ensure(E + 1)) ||
+        (rc = ctx->a_ptr.ensure(G + 2)) ||
         (rc = ctx->a_cnt.ensure(2)) || (rc = ctx->a_stage.ensure(((size_t)2 * (G + 2) + E + 4) * sizeof(uint32_t))))
         return rc;
     uint32_t *hs = static_cast<uint32_t *>(ctx->a_stage.p);
@@ -1396,10 +1414,11 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         HIPCHECK(hipGetLastError());
     }
     hipLaunchKernelGGL(ung_addl_count_kernel, dim3(eb), dim3(256), 0, sm0, ctx->a_gb.p, ctx->a_oi.p, ctx->a_eg.p,
-                       ctx->a_reached.p, E, num_cross, ctx->a_rows.p, ctx->a_edges.p, ctx->a_cnt.p);
+                       ctx->a_reached.p, E, num_cross, ctx->a_rows.p, ctx->a_edges.p, ctx->a_items.p, ctx->a_cnt.p);
     HIPCHECK(hipGetLastError());
     hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, sm0, ctx->a_rows.p + E, 1u);
     hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, sm0, ctx->a_edges.p + E, 1u);
+    hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, sm0, ctx->a_items.p + E, 1u);
     size_t tmp = 0, tmp2 = 0;
     HIPCHECK(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp, ctx->a_rows.p, ctx->a_rows.p, (int)(E + 1), sm0));
     HIPCHECK(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp2, ctx->a_edges.p, ctx->a_edges.p, (int)(E + 1), sm0));
@@ -1407,13 +1426,21 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         return rc;
     HIPCHECK(hipcub::DeviceScan::ExclusiveSum(ctx->a_tmp.p, tmp, ctx->a_rows.p, ctx->a_rows.p, (int)(E + 1), sm0));
     HIPCHECK(hipcub::DeviceScan::ExclusiveSum(ctx->a_tmp.p, tmp2, ctx->a_edges.p, ctx->a_edges.p, (int)(E + 1), sm0));
-    uint32_t totals[2] = {0, 0};
+    HIPCHECK(hipcub::DeviceScan::ExclusiveSum(ctx->a_tmp.p, tmp2, ctx->a_items.p, ctx->a_items.p, (int)(E + 1), sm0));
+    uint32_t totals[3] = {0, 0, 0};
     unsigned long long cnt[2] = {0, 0};
     HIPCHECK(hipMemcpyAsync(&totals[0], ctx->a_rows.p + E, sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
     HIPCHECK(hipMemcpyAsync(&totals[1], ctx->a_edges.p + E, sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
+    HIPCHECK(hipMemcpyAsync(&totals[2], ctx->a_items.p + E, sizeof(uint32_t), hipMemcpyDeviceToHost, sm0));
     HIPCHECK(hipMemcpyAsync(cnt, ctx->a_cnt.p, sizeof(cnt), hipMemcpyDeviceToHost, sm0));
     HIPCHECK(hipStreamSynchronize(sm0));
-    const uint32_t R = totals[0];
+    const uint32_t R = totals[0], I = totals[2];
+    // the scan items (at most R + pairs / ADDL_RANGE) were counted in 32 bits
+    if ((uint64_t)R + cnt[0] / ADDL_RANGE >= 0xFFFFFFFFull) {
+        set_error("ung_hip_additional_edges: %llu target vectors to scan exceed 32-bit item counts",
+                  (unsigned long long)cnt[0]);
+        return UNG_HIP_EINVAL;
+    }
     const uint64_t total_edges = totals[1];
     *n_edges = total_edges;
     if (st)
@@ -1424,7 +1451,10 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         return UNG_HIP_EINVAL;
     }
     // step 3: the scans, written in place; per-group offsets
-    if ((rc = ctx->a_from.ensure(total_edges + 1)) || (rc = ctx->a_to.ensure(total_edges + 1)))
+    const uint32_t per_max = num_cross / 2;
+    if ((rc = ctx->a_from.ensure(total_edges + 1)) || (rc = ctx->a_to.ensure(total_edges + 1)) ||
+        (rc = ctx->a_ientry.ensure((uint64_t)I + 1)) || (rc = ctx->a_pid.ensure((uint64_t)I * per_max + 1)) ||
+        (rc = ctx->a_pdist.ensure((uint64_t)I * per_max + 1)))
         return rc;
     HIPCHECK(hipEventRecord(ctx->ev[1], sm0));
     if (R > 0) {
@@ -1436,14 +1466,24 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         A.eg = ctx->a_eg.p;
         A.row_off = ctx->a_rows.p;
         A.edge_off = ctx->a_edges.p;
+        A.item_off = ctx->a_items.p;
+        A.item_entry = ctx->a_ientry.p;
         A.E = E;
-        A.per_max = num_cross / 2;
+        A.I = I;
+        A.per_max = per_max;
+        A.part_ids = ctx->a_pid.p;
+        A.part_dist = ctx->a_pdist.p;
         A.from = ctx->a_from.p;
         A.to = ctx->a_to.p;
         hipLaunchKernelGGL(ung_addl_small_kernel, dim3((E + 255) / 256), dim3(256), 0, sm0, A);
         HIPCHECK(hipGetLastError());
-        hipLaunchKernelGGL(ung_addl_scan_kernel, dim3(std::min<uint32_t>(E, 65536u)), dim3(64), 0, sm0, A);
-        HIPCHECK(hipGetLastError());
+        if (I > 0) {
+            hipLaunchKernelGGL(ung_addl_expand_kernel, dim3(std::min<uint32_t>((E + 255) / 256, 65535u)), dim3(256), 0,
+                               sm0, ctx->a_items.p, E, ctx->a_ientry.p);
+            hipLaunchKernelGGL(ung_addl_scan_kernel, dim3(std::min<uint32_t>(I, 262144u)), dim3(64), 0, sm0, A);
+            hipLaunchKernelGGL(ung_addl_merge_kernel, dim3(std::min<uint32_t>(I, 65536u)), dim3(64), 0, sm0, A);
+            HIPCHECK(hipGetLastError());
+        }
     }
     hipLaunchKernelGGL(ung_addl_ptr_kernel, dim3((G + 2 + 255) / 256), dim3(256), 0, sm0, ctx->a_op.p, ctx->a_edges.p,
                        G, ctx->a_ptr.p);
