@@ -720,28 +720,24 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     [[maybe_unused]] __amdgpu_buffer_rsrc_t qres, xres;
     [[maybe_unused]] uint32_t xoff[LM];
     [[maybe_unused]] const uint32_t *xrow[LM];
-    if constexpr (MODE == LOAD_BUF32) {
+    if constexpr (MODE == LOAD_BUF32)
         xres = __builtin_amdgcn_make_buffer_rsrc((void *)XS, (short)0, (int)P.x_bytes, 0x00020000);
-    } else {
-        qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * dp), (short)0, (int)(qcnt * dp * 4u),
-                                                 0x00020000);
-    }
-    // query rows lr0 + RSTEP*m: one vector offset, the row steps as scalar offsets.  Rows
-    // past the item's queries (padding columns, whose results are never read) load
-    // whatever the buffer holds there, zero beyond its range.
+    // the item's query rows: a buffer of exactly qcnt rows, so that rows past them
+    // (padding columns, whose results are never read) read zeros without touching memory
+    qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * dp), (short)0, (int)(qcnt * dp * 4u),
+                                             0x00020000);
+    // query rows lr0 + RSTEP*m: one vector offset, the row steps as scalar offsets
     const uint32_t qrow_step = (uint32_t)RSTEP * dp * 4u;
-    const uint32_t qoff = MODE == LOAD_BUF32 ? ((q0 + (uint32_t)lr0) * dp + (uint32_t)c4) * 4u
-                                             : ((uint32_t)lr0 * dp + (uint32_t)c4) * 4u;
+    const uint32_t qoff = ((uint32_t)lr0 * dp + (uint32_t)c4) * 4u;
 
     // register-query layout: the high words of this lane's query columns (k-block kb:
     // chunk kb/2, float4 column 2*(kb%2) + h of the chunk row) and the low words of all
     // the item's queries (float4 column 4*chunk + c of row q) into LDS
     [[maybe_unused]] bf16x8 bhr[2 * QR_NK][NB];
     if constexpr (QR) {
-        // 32-bit loads: rows of the whole split set; wide loads: rows of the item's queries
-        // (q0 = 0 in that buffer, zeros past its qcnt rows)
-        const __amdgpu_buffer_rsrc_t qr_res = MODE == LOAD_BUF32 ? xres : qres;
-        const uint32_t qr0 = MODE == LOAD_BUF32 ? q0 : 0u;
+        // rows of the item's queries (row 0 of qres is query q0; zeros past its qcnt rows)
+        const __amdgpu_buffer_rsrc_t qr_res = qres;
+        const uint32_t qr0 = 0u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const uint32_t row = qr0 + (uint32_t)(wn * QW + 32 * nb + r);
@@ -792,7 +788,7 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
         for (int m = 0; m < LM; ++m) {
             if constexpr (MODE == LOAD_BUF32) {
                 if constexpr (!QR)
-                    rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, qoff, kc * 4u + m * qrow_step, 0));
+                    rq[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, qoff, kc * 4u + m * qrow_step, 0));
                 rx[m] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[m], kc * 4u, 0));
             } else {
                 if constexpr (!QR)
@@ -2550,9 +2546,15 @@ __global__ void ung_addl_count_kernel(const uint32_t *__restrict__ gb, const uin
         edges[p] = m * per;
         items[p] = nx > ADDL_SMALL ? m * ((nx + ADDL_RANGE - 1) / ADDL_RANGE) : 0u;
     }
-    if (my_pairs)
+    // one atomic per wave and counter (same-address atomics serialise in the L2)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        my_pairs += __shfl_xor(my_pairs, o);
+        my_entries += __shfl_xor(my_entries, o);
+    }
+    if ((threadIdx.x & 63u) == 0 && my_pairs)
         atomicAdd(&cnt[0], my_pairs);
-    if (my_entries)
+    if ((threadIdx.x & 63u) == 0 && my_entries)
         atomicAdd(&cnt[1], my_entries);
 }
 
@@ -2724,59 +2726,71 @@ __global__ __launch_bounds__(64) void ung_addl_merge_kernel(AddlParams A)
     }
 }
 
-// Additional edges, step 3 for target groups of at most ADDL_SMALL vectors: one thread per
-// LNG entry scans them for each of the entry's query rows (all candidates exact, ordered
-// by (dist, id) with an insertion network), writing the first `per` of each row; the wave
-// kernel above skips these rows.
+// Additional edges, step 3 for target groups of at most ADDL_SMALL vectors: one wave per
+// LNG entry.  Its m x nx (query row, target vector) pairs are scored by groups of 8 lanes
+// in the reference's summation order (coalesced 32-byte row segments), then lane j < m
+// orders row j's nx candidates by (dist, id) with an insertion network and writes the
+// first `per`; the wave kernel above skips these rows.  m x nx <= num_cross + ADDL_SMALL
+// - 1 (per = nx when nx <= num_cross / 2, else m <= 3), below ADDL_SMALL_PAIRS for
+// num_cross <= 64.
+constexpr uint32_t ADDL_SMALL_PAIRS = 72;
 
 __global__ __launch_bounds__(256) void ung_addl_small_kernel(AddlParams A)
 {
-    const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= A.E)
-        return;
-    const uint32_t m = A.row_off[p + 1] - A.row_off[p];
-    if (m == 0)
-        return;
-    const uint32_t c = A.eg[p], x = A.oi[p];
-    const uint32_t x0 = A.gb[x], nx = A.gb[x + 1] - x0;
-    if (nx > ADDL_SMALL)
-        return;
-    const uint32_t per = min(nx, A.per_max);
-    for (uint32_t j = 0; j < m; ++j) {
-        const uint32_t q = A.gb[c] + j;
-        const float *qv = A.X + (size_t)q * A.d;
-        float dv[ADDL_SMALL];
-        uint32_t iv[ADDL_SMALL];
-#pragma unroll
-        for (uint32_t t = 0; t < ADDL_SMALL; ++t) {
-            dv[t] = INFINITY;
-            iv[t] = NONE;
-            if (t < nx) {
-                dv[t] = l2_ref_lane(qv, A.X + (size_t)(x0 + t) * A.d, A.d);
-                iv[t] = x0 + t;
-            }
-        }
-        // insertion network under (dist, id): candidates arrive in id order
-#pragma unroll
-        for (int t = 1; t < (int)ADDL_SMALL; ++t)
-#pragma unroll
-            for (int u = t; u > 0; --u)
-                if (cand_less(dv[u], iv[u], dv[u - 1], iv[u - 1])) {
-                    const float td = dv[u];
-                    dv[u] = dv[u - 1];
-                    dv[u - 1] = td;
-                    const uint32_t ti = iv[u];
-                    iv[u] = iv[u - 1];
-                    iv[u - 1] = ti;
-                }
-        const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
-#pragma unroll
-        for (uint32_t t = 0; t < ADDL_SMALL; ++t)
-            if (t < per) {
-                A.from[o + t] = q;
-                A.to[o + t] = iv[t];
-            }
+    __shared__ float sd[4][ADDL_SMALL_PAIRS];
+    const int w = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    const int sg = lane >> 3, sub = lane & 7;
+    const uint32_t p = blockIdx.x * 4u + (uint32_t)w;
+    uint32_t m = 0, nx = 0, x0 = 0, q0 = 0;
+    if (p < A.E) {
+        m = A.row_off[p + 1] - A.row_off[p];
+        const uint32_t x = A.oi[p];
+        x0 = A.gb[x];
+        nx = A.gb[x + 1] - x0;
+        if (nx > ADDL_SMALL)
+            m = 0;
+        if (m > 0)
+            q0 = A.gb[A.eg[p]];
     }
+    const uint32_t np = m * nx;
+    for (uint32_t i = (uint32_t)sg; i < np; i += 8u) {
+        const uint32_t j = i / nx, t = i - j * nx;
+        const float v = l2_ref_8lane(A.X + (size_t)(q0 + j) * A.d, A.X + (size_t)(x0 + t) * A.d, A.d, sub);
+        if (sub == 0)
+            sd[w][i] = v;
+    }
+    __syncthreads();
+    if ((uint32_t)lane >= m)
+        return;
+    const uint32_t j = (uint32_t)lane;
+    float dv[ADDL_SMALL];
+    uint32_t iv[ADDL_SMALL];
+#pragma unroll
+    for (uint32_t t = 0; t < ADDL_SMALL; ++t) {
+        dv[t] = t < nx ? sd[w][j * nx + t] : INFINITY;
+        iv[t] = t < nx ? x0 + t : NONE;
+    }
+    // insertion network under (dist, id): candidates arrive in id order
+#pragma unroll
+    for (int t = 1; t < (int)ADDL_SMALL; ++t)
+#pragma unroll
+        for (int u = t; u > 0; --u)
+            if (cand_less(dv[u], iv[u], dv[u - 1], iv[u - 1])) {
+                const float td = dv[u];
+                dv[u] = dv[u - 1];
+                dv[u - 1] = td;
+                const uint32_t ti = iv[u];
+                iv[u] = iv[u - 1];
+                iv[u - 1] = ti;
+            }
+    const uint32_t per = min(nx, A.per_max);
+    const size_t o = (size_t)A.edge_off[p] + (size_t)j * per;
+#pragma unroll
+    for (uint32_t t = 0; t < ADDL_SMALL; ++t)
+        if (t < per) {
+            A.from[o + t] = q0 + j;
+            A.to[o + t] = iv[t];
+        }
 }
 
 // edge_ptr[c] = first edge of group c: the edge offset of its first LNG entry.

@@ -1475,7 +1475,7 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         A.part_dist = ctx->a_pdist.p;
         A.from = ctx->a_from.p;
         A.to = ctx->a_to.p;
-        hipLaunchKernelGGL(ung_addl_small_kernel, dim3((E + 255) / 256), dim3(256), 0, sm0, A);
+        hipLaunchKernelGGL(ung_addl_small_kernel, dim3((E + 3) / 4), dim3(256), 0, sm0, A);
         HIPCHECK(hipGetLastError());
         if (I > 0) {
             hipLaunchKernelGGL(ung_addl_expand_kernel, dim3(std::min<uint32_t>((E + 255) / 256, 65535u)), dim3(256), 0,
