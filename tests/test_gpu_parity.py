@@ -286,6 +286,28 @@ def test_additional_edges_closed_form_problem(ctx, oracle, k):
     assert (got[1].size == 0) == (k < 2)
 
 
+@pytest.mark.parametrize("nx", [7, 8, 5, 1])
+def test_additional_edges_small_target_k64(ctx, oracle, nx):
+    """k = 64 and a target group of nx <= 8 vectors that no cross edge reaches: the entry
+    scores m * nx = ceil(64 / nx) * nx (up to 70) (query row, vector) pairs in one wave,
+    the most the small-target kernel takes."""
+    rng = np.random.default_rng(40 + nx)
+    nc, n1, d = 70, 100, 16
+    X = np.concatenate([rng.standard_normal((nc + n1, d)) * 0.1,
+                        rng.standard_normal((nx, d)) * 0.1 + 50.0]).astype(np.float32)
+    gb = np.array([0, 0, nc, nc + n1, nc + n1 + nx], np.uint32)
+    op = np.array([0, 0, 2, 2, 2], np.uint32)
+    oi = np.array([2, 3], np.uint32)  # C -> (the near group, the far small group)
+    ctx.prepare_vectors(X)
+    ids, _, _, _ = ctx.cross_topk(gb, op, oi, 64)
+    got = ctx.additional_edges(gb, op, oi, 64)
+    want = oracle.additional_edges(X, gb, op, oi, ids, 64)
+    m = min(nc, -(-64 // nx))
+    _say(f"small target nx={nx}: {got[1].size} edges ({m} query rows)")
+    assert got[1].size == m * nx
+    _assert_edges_equal(got, want, f"small target nx={nx} k=64")
+
+
 def test_additional_edges_errors(ctx):
     X = np.zeros((10, 8), np.float32)
     ctx.prepare_vectors(X)
