@@ -724,12 +724,18 @@ int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t 
     M.out_size = m.out_size;
     M.flag_count = m.flag_count;
     M.flagged = m.flagged;
+    // group kNN plans (exclusive jobs: a group against itself) of long rows spread their
+    // items over the XCDs in contiguous ranges (d = 768: intra merge 11.3 -> 8.5 ms; at
+    // d = 128 and 384 it measured the same or 2 % slower)
+    M.xcd_spread = (pl.jobs[0].flags & 1u) != 0 && ctx->d >= 512 ? 1u : 0u;
     const uint32_t n_m = (uint32_t)pl.n_mitems;
     for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
         MergeParams Mc = M;
         Mc.mitems = M.mitems + off;
         const uint32_t n = std::min<uint32_t>(1u << 30, n_m - off);
-        hipLaunchKernelGGL(ung_merge_kernel, dim3(n), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
+        Mc.n_mitems = n;
+        const uint32_t grid = M.xcd_spread ? NUM_XCD * ((n + NUM_XCD - 1u) / NUM_XCD) : n;
+        hipLaunchKernelGGL(ung_merge_kernel, dim3(grid), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
         HIPCHECK(hipGetLastError());
     }
     HIPCHECK(hipEventRecord(ws.ev[2], ws.stream));
