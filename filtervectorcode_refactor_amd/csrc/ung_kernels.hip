@@ -18,6 +18,8 @@
 //             candidate left out can enter the top-k.
 //   fallback: rows whose bound does not certify the result are rescanned exactly
 //             (rare; counted in ung_hip_stats::fallback_rows).
+//   tiny    : cross jobs of a few queries and a small union skip the select and the
+//             merge: one wave scores all their (query, candidate) pairs exactly.
 //
 // Reference semantics reproduced: src/uni_nav_graph_cross_edges.cpp:32-57,154-220
 // (cross edges), src/uni_nav_graph_special_blocks.cpp:70-111 (intra exact kNN),
@@ -2342,6 +2344,94 @@ __global__ __launch_bounds__(64) void ung_fallback_kernel(FallbackParams F)
         if (S == 1 && lane == 0 && F.out_size)
             F.out_size[orow] = (int32_t)count;
         __syncthreads();
+    }
+}
+
+// Cross jobs whose q query rows times ceil(U / 64) candidate rounds stay within
+// TINY_ROUNDS (U <= TINY_U) are scanned exactly, one wave per job
+// (ung_tiny_jobs_kernel), instead of by the select and the merge: their 128 x 128 tiles
+// are mostly padding (cfg3: most jobs have 1-4 queries and a few dozen candidates), and
+// their exact scan costs less than their tiles.
+constexpr uint32_t TINY_U = 1024;
+constexpr uint32_t TINY_ROUNDS = 8;
+constexpr uint32_t TINY_PAIRS = 64 * TINY_ROUNDS; // q * U <= q * 64 * ceil(U / 64)
+constexpr int TINY_WAVES = 4;                      // jobs (waves) per block
+__host__ __device__ inline bool tiny_job(uint32_t q, uint64_t u)
+{
+    return u <= TINY_U && (uint64_t)q * ((u + 63) / 64) <= TINY_ROUNDS;
+}
+
+// Those jobs (F.flagged[0 .. *F.flag_count).x, splits = 1): a wave scores the job's
+// q x U (query row, candidate) pairs, one per lane (the reference's summation order),
+// into its LDS slots [row * U + v], then for each row k rounds of a (dist, id) argmin
+// over the lanes' best slots of the row, the winning lane rescanning its slots.
+__global__ __launch_bounds__(64 * TINY_WAVES) void ung_tiny_jobs_kernel(FallbackParams F)
+{
+    __shared__ float td[TINY_WAVES][TINY_PAIRS];
+    __shared__ uint32_t ti[TINY_WAVES][TINY_PAIRS];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t njobs = *F.flag_count, k = F.k;
+    for (uint32_t jt = blockIdx.x * TINY_WAVES + (uint32_t)w; jt < njobs; jt += gridDim.x * TINY_WAVES) {
+        const Job jb = F.jobs[F.flagged[jt].x];
+        const bool excl = (jb.flags & 1u) != 0;
+        const uint32_t U = jb.n_cand;
+        // the planner keeps q * U within TINY_PAIRS (tiny_job); the bound keeps the slots safe
+        const uint32_t Q = U ? min(jb.q_count, TINY_PAIRS / U) : 0u, P = Q * U;
+        for (uint32_t p = (uint32_t)lane; p < P; p += 64) {
+            const uint32_t r = p / U, v = p - r * U;
+            const uint32_t q = jb.q_begin + r;
+            const uint32_t g = cand_id(F.seg_start, F.seg_vend, jb.seg_begin, jb.seg_count, v);
+            const bool ok = !(excl && g == q);
+            td[w][p] = ok ? l2_ref_lane(F.X + (size_t)q * F.d, F.X + (size_t)g * F.d, F.d) : INFINITY;
+            ti[w][p] = ok ? g : NONE;
+        }
+        // the slots of a row were written by other lanes of the wave
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (uint32_t r = 0; r < Q; ++r) {
+            float bd = INFINITY;
+            uint32_t bi = NONE, bp = 0;
+            for (uint32_t v = (uint32_t)lane; v < U; v += 64)
+                if (cand_less(td[w][r * U + v], ti[w][r * U + v], bd, bi)) {
+                    bd = td[w][r * U + v];
+                    bi = ti[w][r * U + v];
+                    bp = r * U + v;
+                }
+            const size_t orow = (size_t)jb.out_row + r;
+            uint32_t count = 0;
+            for (uint32_t t = 0; t < k; ++t) {
+                float md = bd;
+                uint32_t mi = bi;
+                wave_argmin(md, mi);
+                if (mi == NONE)
+                    break; // no candidate left (wave-uniform); the row's rest keeps its fill
+                if (lane == 0) {
+                    F.out_ids[orow * k + t] = mi - jb.id_base;
+                    if (F.out_dist)
+                        F.out_dist[orow * k + t] = md;
+                }
+                ++count;
+                if (bi == mi) { // the winning lane (ids are unique) takes its next best
+                    td[w][bp] = INFINITY;
+                    ti[w][bp] = NONE;
+                    bd = INFINITY;
+                    bi = NONE;
+                    for (uint32_t v = (uint32_t)lane; v < U; v += 64)
+                        if (cand_less(td[w][r * U + v], ti[w][r * U + v], bd, bi)) {
+                            bd = td[w][r * U + v];
+                            bi = ti[w][r * U + v];
+                            bp = r * U + v;
+                        }
+                }
+            }
+            if (lane == 0 && F.out_size)
+                F.out_size[orow] = (int32_t)count;
+        }
+        // the next job rewrites the slots other lanes read above
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 

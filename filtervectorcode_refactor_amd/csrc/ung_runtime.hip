@@ -112,7 +112,12 @@ struct Plan {
     uint64_t padded = 0;
     uint64_t rows = 0;
     uint64_t max_item_cand = 0;    // largest candidate range of an item
+    // jobs of a few queries and a small union (tiny_job), scanned exactly without the
+    // select and the merge (n_split = 0): [0].x = n_tiny, then (job, 0) for each
+    ung::RawVector<uint2> tiny;
+    uint64_t n_tiny = 0;
 };
+
 
 struct ResultBufs {
     DevBuf<uint32_t> ids;
@@ -140,8 +145,8 @@ namespace {
 // items (written after the select kernel is enqueued, so building and uploading them
 // overlaps it); 256-byte aligned parts.
 struct StageLayout {
-    size_t bj, bi, bs, bm;     // bytes of jobs, items, each segment array, merge items
-    size_t oj, oi, os, ov, om; // offsets
+    size_t bj, bi, bs, bt, bm;     // bytes of jobs, items, each segment array, tiny rows, merge items
+    size_t oj, oi, os, ov, ot, om; // offsets
     size_t total;
 };
 
@@ -152,12 +157,14 @@ StageLayout stage_layout(const Plan &pl)
     L.bj = pl.jobs.size() * sizeof(Job);
     L.bi = pl.items.size() * sizeof(Item);
     L.bs = pl.seg_start.size() * sizeof(uint32_t);
+    L.bt = pl.n_tiny ? (pl.n_tiny + 1) * sizeof(uint2) : 0;
     L.bm = pl.n_mitems * sizeof(MergeItem);
     L.oj = 0;
     L.oi = al(L.bj);
     L.os = L.oi + al(L.bi);
     L.ov = L.os + al(L.bs);
-    L.om = L.ov + al(L.bs);
+    L.ot = L.ov + al(L.bs);
+    L.om = L.ot + al(L.bt);
     L.total = L.om + al(L.bm);
     return L;
 }
@@ -173,6 +180,7 @@ struct PlanMem {
     float *part_dist = nullptr, *part_bound = nullptr;
     uint32_t *flag_count = nullptr; // [0]: rows flagged for the rescan, [1]: select item counter
     uint2 *flagged = nullptr;
+    uint2 *tiny = nullptr;          // Plan::tiny
     uint32_t *out_ids = nullptr;    // result rows
     float *out_dist = nullptr;
     int32_t *out_size = nullptr;
@@ -202,6 +210,7 @@ struct Workspace {
     DevBuf<float> part_bound;
     DevBuf<uint32_t> flag_count; // [0]: rows flagged for the rescan, [1]: select item counter
     DevBuf<uint2> flagged;
+    DevBuf<uint2> tiny;
     DevBuf<uint32_t> fb_ids; // rescan range results
     DevBuf<float> fb_dist;
     HostBuf stage;           // pinned staging of the work-list uploads
@@ -218,6 +227,7 @@ struct Workspace {
         part_bound.release();
         flag_count.release();
         flagged.release();
+        tiny.release();
         fb_ids.release();
         fb_dist.release();
     }
@@ -319,6 +329,8 @@ void plan_reset(Plan &pl)
     pl.seg_vend.clear();
     pl.n_mitems = 0;
     pl.max_item_cand = 0;
+    pl.tiny.clear();
+    pl.n_tiny = 0;
     pl.part_rows = 0;
     pl.pairs = 0;
     pl.padded = 0;
@@ -353,6 +365,8 @@ void write_merge_items(const Plan &pl, MergeItem *out)
     size_t n = 0;
     for (uint32_t j = 0; j < (uint32_t)pl.jobs.size(); ++j) {
         const uint32_t qc = pl.jobs[j].q_count;
+        if (pl.jobs[j].n_split == 0)
+            continue; // scanned exactly (Plan::tiny)
         for (uint32_t qo = 0; qo < qc; qo += MERGE_ROWS)
             out[n++] = MergeItem{j, qo, std::min<uint32_t>(MERGE_ROWS, qc - qo), 0u};
     }
@@ -514,7 +528,7 @@ int workspace_mem(Workspace &ws, const Plan &pl, uint32_t lp, ResultBufs &res, P
         (rc = ws.seg_vend.ensure(pl.seg_vend.size())) ||
         (rc = ws.part_ids.ensure(pl.part_rows * lp)) || (rc = ws.part_dist.ensure(pl.part_rows * lp)) ||
         (rc = ws.part_bound.ensure(pl.part_rows)) || (rc = ws.flag_count.ensure(2)) ||
-        (rc = ws.flagged.ensure(std::max<uint64_t>(pl.rows, 1))))
+        (rc = ws.flagged.ensure(std::max<uint64_t>(pl.rows, 1))) || (rc = ws.tiny.ensure(pl.n_tiny + 1)))
         return rc;
     if (!pl.jobs.empty()) {
         // the previous call's uploads from the staging buffer have completed (its merge
@@ -533,6 +547,7 @@ int workspace_mem(Workspace &ws, const Plan &pl, uint32_t lp, ResultBufs &res, P
     m.part_bound = ws.part_bound.p;
     m.flag_count = ws.flag_count.p;
     m.flagged = ws.flagged.p;
+    m.tiny = ws.tiny.p;
     m.out_ids = res.ids.p;
     m.out_dist = res.dist.p;
     m.out_size = res.size.p;
@@ -552,6 +567,8 @@ void stage_plan(ung_hip_ctx *ctx, const Plan &pl, const StageLayout &L, char *hs
     const uint64_t n = pl.items.size();
     const int T = ctx->pool ? ctx->pool->size() : 1;
     Item *sorted = reinterpret_cast<Item *>(hs + L.oi);
+    if (L.bt)
+        std::memcpy(hs + L.ot, pl.tiny.data(), L.bt);
     uint32_t max_t = 0;
     if (n < 65536 || T == 1) {
         std::memcpy(hs + L.oj, pl.jobs.data(), L.bj);
@@ -637,6 +654,8 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
         HIPCHECK(hipMemcpyAsync(m.items, hs + L.oi, L.bi, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(m.seg_start, hs + L.os, L.bs, hipMemcpyHostToDevice, ws.stream));
         HIPCHECK(hipMemcpyAsync(m.seg_vend, hs + L.ov, L.bs, hipMemcpyHostToDevice, ws.stream));
+        if (L.bt)
+            HIPCHECK(hipMemcpyAsync(m.tiny, hs + L.ot, L.bt, hipMemcpyHostToDevice, ws.stream));
     }
     if (st)
         st->h2d_ms += ms_since(t_h2d);
@@ -684,6 +703,26 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
     if (rc)
         return rc;
     HIPCHECK(hipEventRecord(ws.ev[1], ws.stream));
+    if (pl.n_tiny > 0) {
+        // the jobs left out of the select (tiny_job), one wave each, exact
+        FallbackParams F{};
+        F.X = ctx->X;
+        F.d = ctx->d;
+        F.k = k;
+        F.jobs = m.jobs;
+        F.seg_start = m.seg_start;
+        F.seg_vend = m.seg_vend;
+        F.flag_count = reinterpret_cast<const uint32_t *>(m.tiny);
+        F.flagged = m.tiny + 1;
+        F.splits = 1;
+        F.out_ids = m.out_ids;
+        F.out_dist = m.out_dist;
+        F.out_size = m.out_size;
+        const uint64_t blocks = (pl.n_tiny + TINY_WAVES - 1) / TINY_WAVES;
+        hipLaunchKernelGGL(ung_tiny_jobs_kernel, dim3((unsigned)std::min<uint64_t>(blocks, 1u << 20)),
+                           dim3(64 * TINY_WAVES), 0, ws.stream, F);
+        HIPCHECK(hipGetLastError());
+    }
     return plan_launch_merge(ctx, ws, pl, k, m, st);
 }
 
@@ -860,7 +899,7 @@ int check_ready(ung_hip_ctx *ctx)
 // validates its groups; after a prefix over the chunks pass 2 writes them at its offsets.
 struct PlanChunk {
     uint32_t g_begin = 0, g_end = 0; // groups [g_begin, g_end)
-    uint64_t jobs = 0, segs = 0, items = 0, mitems = 0, part_rows = 0, pairs = 0, padded = 0, rows = 0;
+    uint64_t jobs = 0, segs = 0, items = 0, mitems = 0, part_rows = 0, pairs = 0, padded = 0, rows = 0, tiny = 0;
     int rc = UNG_HIP_OK;
     char msg[192] = {};
 };
@@ -938,14 +977,18 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
             }
             if (u == 0)
                 continue;
-            const uint64_t sv = split_size(u), ns = (u + sv - 1) / sv, qb = (qn + BQ - 1) / BQ;
             c.jobs += 1;
             c.segs += segs;
+            c.pairs += (uint64_t)qn * u;
+            c.rows += qn;
+            if (tiny_job(qn, u)) {
+                c.tiny += 1;
+                continue;
+            }
+            const uint64_t sv = split_size(u), ns = (u + sv - 1) / sv, qb = (qn + BQ - 1) / BQ;
             c.items += ns * qb;
             c.mitems += (qn + MERGE_ROWS - 1) / MERGE_ROWS;
             c.part_rows += (uint64_t)qn * ns;
-            c.pairs += (uint64_t)qn * u;
-            c.rows += qn;
             const uint64_t last = u - (ns - 1) * sv;
             c.padded += (uint64_t)BQ * qb * ((ns - 1) * sv + (last + BC - 1) / BC * BC);
         }
@@ -956,7 +999,7 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
     else
         ctx->pool->run(nch, pass1);
     uint64_t n_jobs = 0, n_segs = 0, n_items = 0;
-    std::vector<uint64_t> o_job(nch), o_seg(nch), o_item(nch), o_part(nch);
+    std::vector<uint64_t> o_job(nch), o_seg(nch), o_item(nch), o_part(nch), o_tiny(nch);
     for (uint32_t t = 0; t < nch; ++t) {
         if (ch[t].rc) {
             set_error("%s", ch[t].msg);
@@ -966,6 +1009,8 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
         o_seg[t] = n_segs;
         o_item[t] = n_items;
         o_part[t] = pl.part_rows;
+        o_tiny[t] = pl.n_tiny;
+        pl.n_tiny += ch[t].tiny;
         n_jobs += ch[t].jobs;
         n_segs += ch[t].segs;
         n_items += ch[t].items;
@@ -983,8 +1028,12 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
     pl.items.resize(n_items);
     pl.seg_start.resize(n_segs);
     pl.seg_vend.resize(n_segs);
+    if (pl.n_tiny) {
+        pl.tiny.resize(pl.n_tiny + 1);
+        pl.tiny[0] = make_uint2((uint32_t)pl.n_tiny, 0u);
+    }
     auto pass2 = [&](int64_t t) {
-        uint64_t j = o_job[t], sg = o_seg[t], itn = o_item[t], part = o_part[t];
+        uint64_t j = o_job[t], sg = o_seg[t], itn = o_item[t], part = o_part[t], tn = 1 + o_tiny[t];
         for (uint32_t g = ch[t].g_begin; g < ch[t].g_end; ++g) {
             const uint32_t qn = group_begin[g + 1] - group_begin[g];
             if (qn == 0 || out_ptr[g + 1] == out_ptr[g])
@@ -1009,12 +1058,18 @@ int build_cross_plan(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, 
             jb.seg_begin = (uint32_t)seg0;
             jb.seg_count = (uint32_t)(sg - seg0);
             jb.n_cand = (uint32_t)u;
-            jb.split_v = split_size(u);
-            jb.n_split = (uint32_t)((u + jb.split_v - 1) / jb.split_v);
-            jb.part_base = (uint32_t)part;
             jb.out_row = group_begin[g];
             jb.id_base = 0;
             jb.flags = 0;
+            if (tiny_job(qn, u)) {
+                pl.jobs[j] = jb; // n_split = 0: no items, partial rows or merge
+                pl.tiny[tn++] = make_uint2((uint32_t)j, 0u);
+                ++j;
+                continue;
+            }
+            jb.split_v = split_size(u);
+            jb.n_split = (uint32_t)((u + jb.split_v - 1) / jb.split_v);
+            jb.part_base = (uint32_t)part;
             part += (uint64_t)qn * jb.n_split;
             pl.jobs[j] = jb;
             // split-major: consecutive items are query blocks streaming the same candidates
@@ -1657,6 +1712,7 @@ int scratch_mem(ung_hip_ctx *ctx, const Plan &pl, uint32_t lp, PlanMem &m)
     const uint64_t o_pb = take(pl.part_rows * sizeof(float));
     const uint64_t o_fc = take(2 * sizeof(uint32_t));
     const uint64_t o_fl = take(std::max<uint64_t>(pl.rows, 1) * sizeof(uint2));
+    const uint64_t o_tiny = take((pl.n_tiny + 1) * sizeof(uint2));
     if (off > UNG_HIP_NOALLOC_SCRATCH_BYTES) {
         set_error("ung_hip_cross_topk_noalloc: the call needs %llu bytes of scratch, the maximum is %llu "
                   "(use ung_hip_cross_topk_device)",
@@ -1674,6 +1730,7 @@ int scratch_mem(ung_hip_ctx *ctx, const Plan &pl, uint32_t lp, PlanMem &m)
     m.part_bound = reinterpret_cast<float *>(b + o_pb);
     m.flag_count = reinterpret_cast<uint32_t *>(b + o_fc);
     m.flagged = reinterpret_cast<uint2 *>(b + o_fl);
+    m.tiny = reinterpret_cast<uint2 *>(b + o_tiny);
     const uint64_t rest = UNG_HIP_NOALLOC_SCRATCH_BYTES - off;
     m.fb_grow = false;
     m.fb_cap = rest / (sizeof(uint32_t) + sizeof(float)) / 64 * 64;
