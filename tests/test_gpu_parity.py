@@ -49,6 +49,35 @@ def test_cross_cfg1_bitexact(ctx, cfg1_stage, oracle):
     assert stats["pairs"] == F.count_pairs(st.group_begin, st.out_ptr, st.out_idx)[0]
 
 
+@pytest.mark.parametrize("k", [6, 1, 40])
+def test_cross_tiny_and_tiled_jobs(ctx, oracle, k):
+    """Groups of 1-130 vectors with 0-4 random out-groups: jobs of a few queries and small
+    unions take the exact per-job scan, the others the select and the merge (q = 9 with
+    U <= 64 is just past the tiny bound); unions smaller than k leave rows part-empty;
+    a duplicated vector gives distance ties."""
+    rng = np.random.default_rng(50 + k)
+    sizes = rng.choice([1, 2, 3, 5, 8, 9, 17, 40, 70, 130], size=60)
+    G, d = sizes.size, 40
+    N = int(sizes.sum())
+    X = rng.standard_normal((N, d)).astype(np.float32)
+    X[5] = X[6]
+    gb = np.concatenate([[0, 0], np.cumsum(sizes)]).astype(np.uint32)
+    rows = [[] for _ in range(G + 1)]
+    for g in range(1, G + 1):
+        cand = [x for x in range(1, G + 1) if x != g]
+        rows[g] = sorted(rng.choice(cand, size=int(rng.integers(0, 5)), replace=False).tolist())
+    op = np.zeros(G + 2, np.uint32)
+    op[2:] = np.cumsum([len(rows[g]) for g in range(1, G + 1)])
+    oi = np.array([x for g in range(1, G + 1) for x in rows[g]], np.uint32)
+    ctx.prepare_vectors(X)
+    ids, dist, size, st = ctx.cross_topk(gb, op, oi, k)
+    _say(f"tiny/tiled k={k}: {st['work_items']} select items, {st['rows']} rows")
+    pg = np.repeat(np.arange(1, G + 1, dtype=np.uint32), sizes)
+    o = oracle.cross_exact_points(X, gb, pg, op, oi, np.arange(N, dtype=np.uint32), k)
+    _assert_rows_equal(ids, dist, None, o[0], o[1], None, f"tiny/tiled k={k}")
+    assert np.array_equal(size, (ids != 0xFFFFFFFF).sum(axis=1)), "row sizes"
+
+
 def test_intra_cfg1_bitexact(ctx, cfg1_stage, oracle):
     st = cfg1_stage
     ctx.prepare_vectors(st.base)
