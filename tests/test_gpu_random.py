@@ -40,10 +40,17 @@ def _vectors(rng, n, d, integer):
     return X
 
 
+def _cases(n, dims, ks, seed):
+    """n random (seed, d, k, integer) cases, the same on every run."""
+    rng = np.random.default_rng(seed)
+    return [(i + 1, int(rng.choice(dims)), int(rng.choice(ks)), bool(i % 4 == 3)) for i in range(n)]
+
+
 CROSS_CASES = [  # (seed, d, k, integer coordinates)
     (1, 3, 6, False), (2, 17, 1, False), (3, 64, 16, False), (4, 128, 6, False), (5, 128, 33, True),
     (6, 130, 6, False), (7, 200, 10, True), (8, 384, 64, False), (9, 520, 6, False), (10, 96, 2, True),
-]
+] + [(s + 10, d, k, i) for s, d, k, i in
+     _cases(20, [5, 24, 32, 48, 64, 127, 128, 129, 256, 300, 384, 768], [1, 3, 6, 8, 9, 16, 17, 32, 40, 64], 77)]
 
 
 @pytest.mark.parametrize("seed,d,k,integer", CROSS_CASES)
@@ -73,7 +80,7 @@ def test_random_cross(ctx, oracle, seed, d, k, integer):
 INTRA_CASES = [  # (seed, d, K, integer coordinates)
     (1, 8, 1, False), (2, 32, 8, False), (3, 100, 32, True), (4, 128, 32, False), (5, 128, 50, False),
     (6, 160, 32, False), (7, 384, 16, True), (8, 64, 50, True),
-]
+] + [(s + 8, d, k, i) for s, d, k, i in _cases(12, [7, 16, 40, 96, 128, 192, 384], [1, 2, 6, 10, 20, 32, 45, 50], 78)]
 
 
 @pytest.mark.parametrize("seed,d,K,integer", INTRA_CASES)
