@@ -380,7 +380,7 @@ constexpr int ROW32 = 32 * LDSW;       // 32 panel rows
 
 // Work item of a block, taken from a launch-wide counter when the block starts.  The
 // hardware deals blocks to the 8 XCDs and to their shader engines round-robin by
-// block index, a fixed share each; with item costs from 1 to 128 tiles a fixed share
+// block index, a fixed share each; with item costs from 1 to 256 tiles a fixed share
 // leaves engines idle while others still work.  Taking the next item (items sorted
 // by decreasing cost) when a block actually starts balances the engines.  The grid
 // has exactly n_items blocks, so every block gets one distinct item.
@@ -626,11 +626,11 @@ __device__ __forceinline__ void merge_into_queue32(float (&d)[32], uint32_t (&id
 }
 
 // Operand loads from the split base set (rows of dp words, every chunk whole):
-//   LOAD_BUF32 : split set smaller than 4 GiB -- buffer loads with 32-bit byte offsets;
-//                the k-chunk advances a scalar offset, so the main loop spends no vector
-//                ALU work on addresses;
-//   LOAD_WIDE  : larger -- queries through a buffer based at the item's first query
-//                row, candidates through 64-bit row pointers (one add per load).
+//   LOAD_BUF32 : split set smaller than 4 GiB -- candidate rows by buffer loads with
+//                32-bit byte offsets; the k-chunk advances a scalar offset, so the main
+//                loop spends no vector ALU work on addresses;
+//   LOAD_WIDE  : larger -- candidate rows through 64-bit row pointers (one add per load).
+// In both the item's query rows are read through a buffer of exactly those rows.
 enum : int { LOAD_BUF32 = 1, LOAD_WIDE = 2 };
 
 // Staging area of the NB = 1 layout: each thread's 32 values of its list (row stride 36
@@ -738,23 +738,21 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
     [[maybe_unused]] bf16x8 bhr[2 * QR_NK][NB];
     if constexpr (QR) {
         // rows of the item's queries (row 0 of qres is query q0; zeros past its qcnt rows)
-        const __amdgpu_buffer_rsrc_t qr_res = qres;
-        const uint32_t qr0 = 0u;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const uint32_t row = qr0 + (uint32_t)(wn * QW + 32 * nb + r);
+            const uint32_t row = (uint32_t)(wn * QW + 32 * nb + r);
 #pragma unroll
             for (int kb = 0; kb < 2 * QR_NK; ++kb)
                 bhr[kb][nb] = __builtin_bit_cast(
                     bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                qr_res, (row * dp + (uint32_t)((kb >> 1) * KC + (2 * (kb & 1) + h) * 4)) * 4u, 0, 0));
+                                qres, (row * dp + (uint32_t)((kb >> 1) * KC + (2 * (kb & 1) + h) * 4)) * 4u, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < BQ * QR_NK * 4 / NTH; ++i) {
             const int idx = tid + NTH * i;
             const int q = idx >> 4, f = idx & 15; // f = 4*chunk + float4 column of the low words
-            const uint32_t off = ((qr0 + (uint32_t)q) * dp + (uint32_t)((f >> 2) * KC + 16 + (f & 3) * 4)) * 4u;
-            sm.u.p.qlo[q][f] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qr_res, off, 0, 0));
+            const uint32_t off = ((uint32_t)q * dp + (uint32_t)((f >> 2) * KC + 16 + (f & 3) * 4)) * 4u;
+            sm.u.p.qlo[q][f] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(qres, off, 0, 0));
         }
     }
 
@@ -1456,25 +1454,20 @@ __global__ __launch_bounds__(KNN_THREADS, 1) void ung_knn_select_kernel(SelectPa
     [[maybe_unused]] const uint32_t *xrow[LM];
     if constexpr (MODE == LOAD_BUF32)
         xres = __builtin_amdgcn_make_buffer_rsrc((void *)XS, (short)0, (int)P.x_bytes, 0x00020000);
-    else
-        qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * DP), (short)0, (int)(qcnt * DP * 4u),
-                                                 0x00020000);
+    qres = __builtin_amdgcn_make_buffer_rsrc((void *)(XS + (size_t)q0 * DP), (short)0, (int)(qcnt * DP * 4u),
+                                             0x00020000);
     // this lane's query column for the whole item: the high and low words of every
     // k-block (chunk kc, block kb: float4 column 2*kb + h of the chunk row, +4 for the
-    // low words); columns past the item's queries load zeros or rows never read out
+    // low words); columns past the item's queries load zeros
     bf16x8 qh[NK][2], ql[NK][2];
-    {
-        const __amdgpu_buffer_rsrc_t res = MODE == LOAD_BUF32 ? xres : qres;
-        const uint32_t row = (MODE == LOAD_BUF32 ? q0 : 0u) + (uint32_t)col;
 #pragma unroll
-        for (int kc = 0; kc < NK; ++kc)
+    for (int kc = 0; kc < NK; ++kc)
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const uint32_t off = (row * DP + (uint32_t)(kc * KC + (2 * kb + h) * 4)) * 4u;
-                qh[kc][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(res, off, 0, 0));
-                ql[kc][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(res, off + 64u, 0, 0));
-            }
-    }
+        for (int kb = 0; kb < 2; ++kb) {
+            const uint32_t off = ((uint32_t)col * DP + (uint32_t)(kc * KC + (2 * kb + h) * 4)) * 4u;
+            qh[kc][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qres, off, 0, 0));
+            ql[kc][kb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(qres, off + 64u, 0, 0));
+        }
     auto set_xrows = [&](int slot) {
 #pragma unroll
         for (int m = 0; m < LM; ++m) {
