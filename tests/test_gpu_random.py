@@ -2,7 +2,7 @@
 every row compared bit for bit with the CPU oracle (which is pinned against the
 reference's compiled code by test_oracle.py).
 
-  * cross edges: dimensions 3..520 (one to seventeen 32-dimension chunks: the
+  * cross edges: dimensions 3..768 (one to twenty-four 32-dimension chunks: the
     register-query layout at 128, the restaged panels elsewhere), k from 1 to 64 (queue
     lengths 8, 16 and 32), groups of 1..700 vectors with 0..5 random out-groups (jobs
     from the exact per-job scan to several candidate splits);
