@@ -162,6 +162,61 @@ __device__ __forceinline__ float l2_ref_8lane(const float *__restrict__ a,
     return pair + pair_hi;                   // sub 0: (s0+s1)+(s2+s3)
 }
 
+// l2_ref_8lane for two rows b0, b1 against one row a at once: each value is computed
+// by exactly the operations of l2_ref_8lane (bit-identical), with a's loads shared and
+// twice the loads in flight per block of eight.
+__device__ __forceinline__ void l2_ref_8lane2(const float *__restrict__ a, const float *__restrict__ b0,
+                                              const float *__restrict__ b1, uint32_t d, int sub, float &v0,
+                                              float &v1)
+{
+    float acc0 = 0.0f, acc1 = 0.0f;
+    const uint32_t nb8 = d >> 3;
+    uint32_t blk = 0;
+    for (; blk + 8 <= nb8; blk += 8) {
+        float ta[8], t0[8], t1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            ta[u] = a[8 * (blk + u) + sub];
+            t0[u] = b0[8 * (blk + u) + sub];
+            t1[u] = b1[8 * (blk + u) + sub];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float x0 = ta[u] - t0[u], x1 = ta[u] - t1[u];
+            acc0 = __builtin_fmaf(x0, x0, acc0);
+            acc1 = __builtin_fmaf(x1, x1, acc1);
+        }
+    }
+    for (; blk < nb8; ++blk) {
+        const float av = a[8 * blk + sub];
+        const float x0 = av - b0[8 * blk + sub], x1 = av - b1[8 * blk + sub];
+        acc0 = __builtin_fmaf(x0, x0, acc0);
+        acc1 = __builtin_fmaf(x1, x1, acc1);
+    }
+    float s0 = __shfl_xor(acc0, 4, 8) + acc0;
+    float s1 = __shfl_xor(acc1, 4, 8) + acc1;
+    uint32_t p = nb8 * 8, rem = d - p;
+    if (rem >= 4) {
+        if (sub < 4) {
+            const float av = a[p + sub];
+            const float x0 = av - b0[p + sub], x1 = av - b1[p + sub];
+            s0 = __builtin_fmaf(x0, x0, s0);
+            s1 = __builtin_fmaf(x1, x1, s1);
+        }
+        p += 4;
+        rem -= 4;
+    }
+    if ((uint32_t)sub < rem) {
+        const float av = a[p + sub];
+        const float x0 = av - b0[p + sub], x1 = av - b1[p + sub];
+        s0 = __builtin_fmaf(x0, x0, s0);
+        s1 = __builtin_fmaf(x1, x1, s1);
+    }
+    const float pr0 = s0 + __shfl_xor(s0, 1, 8), pr1 = s1 + __shfl_xor(s1, 1, 8);
+    v0 = pr0 + __shfl_xor(pr0, 2, 8);
+    v1 = pr1 + __shfl_xor(pr1, 2, 8);
+}
+
 // Same value computed by one lane alone.  Rows 16-byte aligned (d % 4 == 0) are read
 // with float4 loads; the accumulation order is the same either way.
 __device__ __forceinline__ float l2_ref_lane(const float *__restrict__ a,
@@ -1935,7 +1990,11 @@ constexpr uint32_t NUM_XCD = 8;
 // One wave per result row: k-way merge of the row's S partial rows (S <= 64, each
 // sorted by approximate distance) to its Lp best approximate candidates, exact
 // re-score of those in the reference's summation order, (dist, id) ranking, and the
-// certificate  T_k < lower bound of every candidate left out.
+// certificate  T_k < lower bound of every candidate left out.  PAIR: each eight-lane
+// group re-scores two candidates per pass (long rows of large d: group kNN lists at
+// d >= 256, 10 % faster there; more registers, which cost the short cross rows and
+// d = 128 more than the shared loads gain).
+template <bool PAIR>
 __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams M)
 {
     __shared__ uint32_t mrank[MERGE_ROWS][128]; // a wave's candidates in rank order
@@ -2145,10 +2204,40 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
             ci[h] = NONE; // left out (exact distance > T): not a result
 
     // exact re-score: 8 lanes per candidate (one per accumulator of the reference's
-    // summation), 8 candidates per pass; candidate t's value goes to lane t % 64, slot t / 64
+    // summation), 8 candidates per pass (PAIR: 16); candidate t's value goes to lane
+    // t % 64, slot t / 64
     const float *qv = M.X + (size_t)q * M.d;
     float ex[2] = {INFINITY, INFINITY};
-    {
+    if constexpr (PAIR) {
+        // group g scores candidates 16p + g and 16p + 8 + g (t < 128: Lp <= 128); lane L
+        // takes candidate 8 (2p + e) + L % 8 from group L % 8, e = 0, 1
+        const int g = lane >> 3, sub = lane & 7;
+        const uint32_t npass = (m_need + 15u) / 16u;
+        for (uint32_t p = 0; p < npass; ++p) {
+            const uint32_t t0 = 16u * p + (uint32_t)g, t1 = t0 + 8u;
+            const uint32_t c0 = t0 < 64u ? __shfl(ci[0], (int)(t0 & 63u)) : __shfl(ci[1], (int)(t0 & 63u));
+            const uint32_t c1 = t1 < 64u ? __shfl(ci[0], (int)(t1 & 63u)) : __shfl(ci[1], (int)(t1 & 63u));
+            const bool ok0 = t0 < Lp && c0 != NONE, ok1 = t1 < Lp && c1 != NONE;
+            float v0, v1 = INFINITY;
+            if (16u * p + 8u < m_need) // wave-uniform: the pass's second half holds candidates
+                l2_ref_8lane2(qv, M.X + (size_t)(ok0 ? c0 : q) * M.d, M.X + (size_t)(ok1 ? c1 : q) * M.d, M.d,
+                              sub, v0, v1);
+            else
+                v0 = l2_ref_8lane(qv, M.X + (size_t)(ok0 ? c0 : q) * M.d, M.d, sub);
+            const float got0 = __shfl(v0, 8 * (lane & 7)), got1 = __shfl(v1, 8 * (lane & 7));
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t pp = 2u * p + (uint32_t)e; // candidates 8pp .. 8pp + 7
+                if ((uint32_t)g == (pp & 7u)) {
+                    const float got = e == 0 ? got0 : got1;
+                    if (pp < 8u)
+                        ex[0] = ci[0] != NONE ? got : INFINITY;
+                    else
+                        ex[1] = ci[1] != NONE ? got : INFINITY;
+                }
+            }
+        }
+    } else {
         const int g = lane >> 3, sub = lane & 7;
         const uint32_t npass = (m_need + 7u) / 8u;
         for (uint32_t p = 0; p < npass; ++p) {
@@ -3035,6 +3124,8 @@ __global__ __launch_bounds__(256) void ung_reverse_kernel(PruneParams K)
     }
 }
 
+constexpr uint32_t PRUNE_LDS_D = 1024;
+
 // One wave (block) per row: forward candidates + the reverse_cap nearest reverse edges,
 // merged by (dist, id) without duplicates, then the greedy alpha scan.
 __global__ __launch_bounds__(64) void ung_prune_kernel(PruneParams K)
@@ -3045,6 +3136,9 @@ __global__ __launch_bounds__(64) void ung_prune_kernel(PruneParams K)
     __shared__ uint32_t ri[32];
     __shared__ uint32_t kept[64];
     __shared__ uint32_t ncand;
+    // the candidate's row, staged once per candidate and read by every pivot's distance
+    // (rows of up to PRUNE_LDS_D floats; larger ones are read from memory each time)
+    __shared__ __align__(16) float trow[PRUNE_LDS_D];
     const int lane = threadIdx.x;
     const uint64_t r = blockIdx.x;
     if (r >= K.rows)
@@ -3093,6 +3187,8 @@ __global__ __launch_bounds__(64) void ung_prune_kernel(PruneParams K)
     const uint32_t nc = ncand;
     const float *__restrict__ X = K.X + (size_t)jb.q_begin * K.d;
     const int g = lane >> 3, sub = lane & 7;
+    // float4 staging: rows 16-byte aligned (d % 4 == 0) that fit
+    const bool stage_t = (K.d & 3u) == 0u && K.d <= (uint32_t)PRUNE_LDS_D;
     uint32_t na = 0;
     for (uint32_t c = 0; c < nc && na < K.final_degree; ++c) {
         const uint32_t t = ci[c];
@@ -3100,11 +3196,21 @@ __global__ __launch_bounds__(64) void ung_prune_kernel(PruneParams K)
         if (t == s)
             continue;
         bool reject = false;
+        if (na > 0 && stage_t) {
+            // one wave per block: the barrier orders the previous candidate's reads of
+            // trow before these writes, and these writes before the reads below
+            __syncthreads();
+            const float4 *src = reinterpret_cast<const float4 *>(X + (size_t)t * K.d);
+            for (uint32_t i = (uint32_t)lane; i < (K.d >> 2); i += 64u)
+                reinterpret_cast<float4 *>(trow)[i] = src[i];
+            __syncthreads();
+        }
         for (uint32_t p0 = 0; p0 < na && !reject; p0 += 8) {
             const uint32_t p = p0 + (uint32_t)g;
             const bool valid = p < na;
             const uint32_t piv = valid ? kept[p] : t;
-            const float dij = l2_ref_8lane(X + (size_t)piv * K.d, X + (size_t)t * K.d, K.d, sub);
+            const float dij = stage_t ? l2_ref_8lane(X + (size_t)piv * K.d, trow, K.d, sub)
+                                      : l2_ref_8lane(X + (size_t)piv * K.d, X + (size_t)t * K.d, K.d, sub);
             reject = __ballot(valid && sub == 0 && K.alpha * dij < dc) != 0;
         }
         if (!reject) {

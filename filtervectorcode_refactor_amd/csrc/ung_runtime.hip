@@ -766,7 +766,11 @@ int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t 
     // group kNN plans (exclusive jobs: a group against itself) of long rows spread their
     // items over the XCDs in contiguous ranges (d = 768: intra merge 11.3 -> 8.5 ms; at
     // d = 128 and 384 it measured the same or 2 % slower)
-    M.xcd_spread = (pl.jobs[0].flags & 1u) != 0 && ctx->d >= 512 ? 1u : 0u;
+    const bool group_plan = (pl.jobs[0].flags & 1u) != 0;
+    M.xcd_spread = group_plan && ctx->d >= 512 ? 1u : 0u;
+    // two candidates per re-score pass for group kNN rows of d >= 256 (cfg3 intra merge
+    // 1.28 -> 1.14 ms, cfg4 8.58 -> 7.71 ms; at d = 128 and in the cross merge slower)
+    const bool pair = group_plan && ctx->d >= 256;
     const uint32_t n_m = (uint32_t)pl.n_mitems;
     for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
         MergeParams Mc = M;
@@ -774,7 +778,10 @@ int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t 
         const uint32_t n = std::min<uint32_t>(1u << 30, n_m - off);
         Mc.n_mitems = n;
         const uint32_t grid = M.xcd_spread ? NUM_XCD * ((n + NUM_XCD - 1u) / NUM_XCD) : n;
-        hipLaunchKernelGGL(ung_merge_kernel, dim3(grid), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
+        if (pair)
+            hipLaunchKernelGGL(ung_merge_kernel<true>, dim3(grid), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
+        else
+            hipLaunchKernelGGL(ung_merge_kernel<false>, dim3(grid), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
         HIPCHECK(hipGetLastError());
     }
     HIPCHECK(hipEventRecord(ws.ev[2], ws.stream));
