@@ -383,10 +383,13 @@ void add_pack_items(Plan &pl)
 }
 
 // Entries per partial row: the k results plus a margin, at most two per merge lane
-// and at most the 4 queues' entries.
-uint32_t pick_lp(uint32_t k, int lt)
+// and at most the 4 queues' entries.  The certified error bound grows with d; from
+// d = 512 a margin of 10 keeps the first value left out far enough above the k-th
+// that few rows need the exact rescan (cfg4: 133 rescanned cross rows, 4.5 ms, with a
+// margin of 4), while at d = 128 the longer rows cost more than the rescans they save.
+uint32_t pick_lp(uint32_t k, int lt, uint32_t d)
 {
-    const uint32_t margin = std::max<uint32_t>(4u, k / 4);
+    const uint32_t margin = std::max<uint32_t>(d >= 512u ? 10u : 4u, k / 4);
     return std::min<uint32_t>(std::min<uint32_t>(128u, 4u * (uint32_t)lt), k + margin);
 }
 
@@ -644,7 +647,7 @@ int plan_launch(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Pla
 {
     int rc;
     const int lt = pick_lt(k);
-    const uint32_t lp = pick_lp(k, lt);
+    const uint32_t lp = pick_lp(k, lt, ctx->d);
     const auto t_h2d = clk::now();
     const StageLayout L = stage_layout(pl);
     char *hs = m.stage;
@@ -731,7 +734,7 @@ int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t 
 {
     if (pl.jobs.empty())
         return UNG_HIP_OK;
-    const uint32_t lp = pick_lp(k, pick_lt(k));
+    const uint32_t lp = pick_lp(k, pick_lt(k), ctx->d);
     const StageLayout L = stage_layout(pl);
     char *hs = m.stage;
     // merge items, built and uploaded (on the upload stream) while the select kernel runs
@@ -884,7 +887,7 @@ int run_plan(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t k, Result
 {
     int rc;
     PlanMem m;
-    if ((rc = workspace_mem(ws, pl, pick_lp(k, pick_lt(k)), res, m)) || (rc = plan_launch(ctx, ws, pl, k, m, st)))
+    if ((rc = workspace_mem(ws, pl, pick_lp(k, pick_lt(k), ctx->d), res, m)) || (rc = plan_launch(ctx, ws, pl, k, m, st)))
         return rc;
     return plan_finish(ctx, ws, pl, k, m, st);
 }
@@ -1208,10 +1211,10 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     // 18.0 ms with the group select alone between the cross merge and the additional edges)
     PlanMem m0;
     if ((rc = cross_prepare_result(ctx, k)) ||
-        (rc = workspace_mem(ctx->ws[0], pl, pick_lp(k, pick_lt(k)), ctx->cross, m0)) ||
+        (rc = workspace_mem(ctx->ws[0], pl, pick_lp(k, pick_lt(k), ctx->d), ctx->cross, m0)) ||
         (rc = plan_launch(ctx, ctx->ws[0], pl, k, m0, st)) ||
         (rc = group_prepare_result(ctx, ctx->intra_plan, list_k)) ||
-        (rc = workspace_mem(ctx->ws[1], ctx->intra_plan, pick_lp(list_k, pick_lt(list_k)), ctx->group,
+        (rc = workspace_mem(ctx->ws[1], ctx->intra_plan, pick_lp(list_k, pick_lt(list_k), ctx->d), ctx->group,
                             ctx->intra_mem)) ||
         (rc = plan_launch(ctx, ctx->ws[1], ctx->intra_plan, list_k, ctx->intra_mem, &ctx->intra_stats,
                           ctx->ws[0].ev[1]))) {
@@ -1785,7 +1788,7 @@ int cross_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, con
     if (st)
         st->plan_ms += ms_since(t0);
     PlanMem m;
-    if ((rc = scratch_mem(ctx, pl, pick_lp(k, pick_lt(k)), m)))
+    if ((rc = scratch_mem(ctx, pl, pick_lp(k, pick_lt(k), ctx->d), m)))
         return rc;
     const size_t stage_bytes = stage_layout(pl).total;
     if (ctx->noalloc_stage.size() < stage_bytes) // host memory, reused by later calls
