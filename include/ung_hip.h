@@ -126,7 +126,7 @@ int ung_hip_cross_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **di
  * partial rows and flags live in a file-scope device array of
  * UNG_HIP_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process ends; a call
  * whose plan needs more returns UNG_HIP_EINVAL (the message gives the bytes needed) --
- * roughly 600k result rows with single-split unions at k = 6.  The call makes no
+ * roughly 600k result rows with single-split unions at k = 6 and d < 512.  The call makes no
  * hipMalloc, hipHostMalloc or hipFree; its host work lists reuse the context's storage.
  * It needs the base set prepared beforehand (ung_hip_prepare_vectors, which allocates, at
  * set-up).  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
