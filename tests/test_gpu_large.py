@@ -49,6 +49,16 @@ def test_prune_random(ctx, oracle, dim, knn_k, fcap, rcap, fd, alpha, seed):
     _check(ctx, oracle, X, [(3, 700), (900, 4500), (5500, 300)], knn_k, fcap, rcap, fd, alpha, "random")
 
 
+@pytest.mark.parametrize("dim,seed", [(768, 5), (1100, 6)])
+def test_prune_large_dim(ctx, oracle, dim, seed):
+    # d = 768: the candidate's row staged in LDS; d = 1100: above the staging size, every
+    # distance reads both rows from memory
+    _say(f"large-group prune dim={dim}")
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((1700, dim)).astype(np.float32)
+    _check(ctx, oracle, X, [(3, 700), (800, 900)], 63, 63, 32, 32, 1.2, f"dim {dim}")
+
+
 def test_prune_integer_ties(ctx, oracle):
     _say("large-group prune, integer data (ties)")
     rng = np.random.default_rng(11)

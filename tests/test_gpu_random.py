@@ -7,7 +7,8 @@ reference's compiled code by test_oracle.py).
     lengths 8, 16 and 32), groups of 1..700 vectors with 0..5 random out-groups (jobs
     from the exact per-job scan to several candidate splits);
   * group kNN: groups of 2..1500 vectors, K from 1 to 50 (filter-and-buffer select at
-    d <= 128, register queues above, and the merge's rank paths);
+    d <= 128, register queues above, and the merge's rank paths; at d >= 256 the merge
+    re-scores two candidates per lane group, checked with dimension tails of 4 to 7);
   * integer coordinates in some cases, so that exact distance ties occur.
 Every call goes through the C ABI."""
 import numpy as np
@@ -80,7 +81,10 @@ def test_random_cross(ctx, oracle, seed, d, k, integer):
 INTRA_CASES = [  # (seed, d, K, integer coordinates)
     (1, 8, 1, False), (2, 32, 8, False), (3, 100, 32, True), (4, 128, 32, False), (5, 128, 50, False),
     (6, 160, 32, False), (7, 384, 16, True), (8, 64, 50, True),
-] + [(s + 8, d, k, i) for s, d, k, i in _cases(12, [7, 16, 40, 96, 128, 192, 384], [1, 2, 6, 10, 20, 32, 45, 50], 78)]
+] + [(s + 8, d, k, i) for s, d, k, i in _cases(12, [7, 16, 40, 96, 128, 192, 384], [1, 2, 6, 10, 20, 32, 45, 50], 78)] + [
+    # d >= 256 (two candidates per re-score pass) with 5, 4 and 7 dimensions past the last
+    # block of eight; 519: the wider partial-row margin and the XCD-contiguous merge
+    (21, 261, 32, False), (22, 300, 20, True), (23, 519, 32, False)]
 
 
 @pytest.mark.parametrize("seed,d,K,integer", INTRA_CASES)
