@@ -102,6 +102,37 @@ def test_noalloc_matches_allocating_entry_point():
             rows.free()
 
 
+def test_noalloc_wide_rows():
+    """d = 520: partial rows keep the wider margin past k (16 entries for k = 6), so the
+    scratch array holds longer rows; two calls, the second on a smaller LNG."""
+    hip = C.CDLL("libamdhip64.so")
+    rng = np.random.default_rng(5)
+    sizes = [300, 40, 2000, 900, 7]
+    gb = np.zeros(len(sizes) + 2, np.uint32)
+    gb[2:] = np.cumsum(sizes)
+    op = np.array([0, 0, 2, 4, 5, 5, 5], np.uint32)   # 1 -> {3, 4}, 2 -> {3, 5}, 3 -> {5}
+    oi = np.array([3, 4, 3, 5, 5], np.uint32)
+    op2 = np.array([0, 0, 1, 1, 1, 1, 1], np.uint32)  # 1 -> {3}
+    oi2 = np.array([3], np.uint32)
+    X = rng.standard_normal((int(gb[-1]), 520)).astype(np.float32)
+    k = 6
+    with F.HipContext(0) as ctx:
+        ctx.prepare_vectors(X)
+        want1 = _expect(ctx, gb, op, oi, k)
+        want2 = _expect(ctx, gb, op2, oi2, k)
+        rows = DeviceRows(hip, X.shape[0], k)
+        try:
+            _say("noalloc d=520 call 1")
+            s1 = ctx.cross_topk_noalloc(gb, op, oi, k, *rows.addrs())
+            _check(rows.download(), want1, "noalloc d=520 call 1")
+            _say("noalloc d=520 call 2 (smaller)")
+            s2 = ctx.cross_topk_noalloc(gb, op2, oi2, k, *rows.addrs())
+            assert s2["pairs"] < s1["pairs"]
+            _check(rows.download(), want2, "noalloc d=520 call 2")
+        finally:
+            rows.free()
+
+
 def test_noalloc_rescan_and_k64():
     """Every row through the exact rescan (a certification bound widened 1e30-fold) with
     unions of several ranges, and k = 64 (the longest partial rows)."""
