@@ -84,6 +84,8 @@ SIGNATURES = {
     "ung_hip_intra_end": (_int, [_vp, _vp]),
     "ung_hip_synchronize": (_int, [_vp]),
     "ung_hip_selftest_mfma": (_int, [_vp, C.POINTER(_dbl)]),
+    "ung_hip_debug_partial_rows": (_int, [_vp, _u64, _vp, _vp, _vp, C.POINTER(_u64), C.POINTER(_dbl),
+                                          C.POINTER(_dbl)]),
     "ung_divide_groups": (_int, [_u64, _vp, _vp, _vp, _vp, _vp, C.POINTER(_u32)]),
     "ung_group_label_sets": (_int, [_u64, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _u64]),
     "ung_lng_build": (_int, [_u32, _vp, _vp, _vp, _vp, _u64, C.POINTER(_u64), _int]),

@@ -116,6 +116,9 @@ struct Plan {
     // select and the merge (n_split = 0): [0].x = n_tiny, then (job, 0) for each
     ung::RawVector<uint2> tiny;
     uint64_t n_tiny = 0;
+    // entries per partial row of the cross call whose partial rows are still in the
+    // first workspace (set when such a call succeeds; 0: none)
+    uint32_t part_lp = 0;
 };
 
 
@@ -331,6 +334,7 @@ void plan_reset(Plan &pl)
     pl.max_item_cand = 0;
     pl.tiny.clear();
     pl.n_tiny = 0;
+    pl.part_lp = 0;
     pl.part_rows = 0;
     pl.pairs = 0;
     pl.padded = 0;
@@ -1169,6 +1173,7 @@ int cross_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, cons
     }
     HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
     ctx->cross.valid = true;
+    pl.part_lp = pick_lp(k, pick_lt(k), ctx->d);
     if (st)
         st->wall_ms += ms_since(t0);
     return UNG_HIP_OK;
@@ -1235,6 +1240,7 @@ int cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
         return rc;
     }
     ctx->cross.valid = true;
+    pl.part_lp = pick_lp(k, pick_lt(k), ctx->d);
     if (st)
         st->wall_ms += ms_since(t0);
     return UNG_HIP_OK;
@@ -1924,6 +1930,7 @@ int ung_hip_release_vectors(ung_hip_ctx *ctx)
     ctx->d = 0;
     ctx->cross.valid = false;
     ctx->group.valid = false;
+    ctx->plan0.part_lp = 0; // partial rows of the released base set
     return UNG_HIP_OK;
 }
 
@@ -2380,6 +2387,69 @@ int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err)
             mx = std::max(mx, std::fabs(ref - (double)host[m * 32 + n]));
         }
     *max_abs_err = mx;
+    return UNG_HIP_OK;
+}
+
+int ung_hip_debug_partial_rows(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *query, uint32_t *cand, float *approx,
+                               uint64_t *n_entries, double *eps_coef, double *rmax)
+{
+    clear_error();
+    if (!ctx || !n_entries) {
+        set_error("ung_hip_debug_partial_rows: null context/n_entries");
+        return UNG_HIP_EINVAL;
+    }
+    const Plan &pl = ctx->plan0;
+    if (pl.part_lp == 0) {
+        set_error("ung_hip_debug_partial_rows: no cross call's partial rows on the device");
+        return UNG_HIP_ESTATE;
+    }
+    int rc;
+    if ((rc = set_device(ctx)))
+        return rc;
+    const uint32_t lp = pl.part_lp;
+    const uint64_t n = pl.part_rows * lp;
+    std::vector<uint32_t> ids(n);
+    std::vector<float> dist(n);
+    if (n) {
+        HIPCHECK(hipMemcpyAsync(ids.data(), ctx->ws[0].part_ids.p, n * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                                ctx->ws[0].stream));
+        HIPCHECK(hipMemcpyAsync(dist.data(), ctx->ws[0].part_dist.p, n * sizeof(float), hipMemcpyDeviceToHost,
+                                ctx->ws[0].stream));
+    }
+    HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
+    // every entry of every job's partial rows: split s, query j at row part_base + s*q_count + j
+    uint64_t cnt = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        cnt = 0;
+        for (const Job &jb : pl.jobs)
+            for (uint32_t sp = 0; sp < jb.n_split; ++sp)
+                for (uint32_t qj = 0; qj < jb.q_count; ++qj) {
+                    const uint64_t prow = (uint64_t)jb.part_base + (uint64_t)sp * jb.q_count + qj;
+                    for (uint32_t e = 0; e < lp; ++e) {
+                        const uint32_t id = ids[prow * lp + e];
+                        if (id == NONE)
+                            continue;
+                        if (pass == 1) {
+                            query[cnt] = jb.q_begin + qj;
+                            cand[cnt] = id;
+                            approx[cnt] = dist[prow * lp + e];
+                        }
+                        ++cnt;
+                    }
+                }
+        if (pass == 0) {
+            *n_entries = cnt;
+            if (eps_coef)
+                *eps_coef = eps_coef_for(ctx->d) * ctx->eps_scale;
+            if (rmax)
+                *rmax = ctx->rmax;
+            if (cnt > capacity || (cnt > 0 && (!query || !cand || !approx))) {
+                set_error("ung_hip_debug_partial_rows: capacity %llu < %llu entries", (unsigned long long)capacity,
+                          (unsigned long long)cnt);
+                return UNG_HIP_EINVAL;
+            }
+        }
+    }
     return UNG_HIP_OK;
 }
 

@@ -263,6 +263,21 @@ class HipContext:
         check(self.lib.ung_hip_selftest_mfma(self.h, C.byref(err)))
         return err.value
 
+    def debug_partial_rows(self):
+        """(query ids, candidate ids, approximate squared distances, eps_coef, rmax) of the
+        last cross-edge call's partial rows (ung_hip_debug_partial_rows; diagnostic)."""
+        n = C.c_uint64(0)
+        ec, rm = C.c_double(), C.c_double()
+        rc = self.lib.ung_hip_debug_partial_rows(self.h, 0, None, None, None, C.byref(n), C.byref(ec), C.byref(rm))
+        if rc != 0 and n.value == 0:
+            check(rc)
+        q = np.empty(n.value, np.uint32)
+        c = np.empty(n.value, np.uint32)
+        a = np.empty(n.value, np.float32)
+        check(self.lib.ung_hip_debug_partial_rows(self.h, n.value, ptr(q), ptr(c), ptr(a), C.byref(n),
+                                                  C.byref(ec), C.byref(rm)))
+        return q, c, a, ec.value, rm.value
+
 
 # ---------------------------------------------------------------------------
 # host-side inputs (C++ in libung_hip.so)

@@ -263,6 +263,19 @@ int ung_hip_synchronize(ung_hip_ctx *ctx);
  * largest deviation from a host-computed product; returns 0 when it ran. */
 int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err);
 
+/* Diagnostic, no counterpart in the reference: the approximate (split-bf16 MFMA,
+ * expansion-form) distances behind the context's last cross-edge call, for checking the
+ * certified error bound against exact distances.  Writes one entry per partial-row
+ * candidate -- query id, candidate id (global ids), approximate squared distance a --
+ * and the bound's constants: |a - D| <= eps_coef * (|q| + rmax)^2 for the exact squared
+ * distance D.  Tiny jobs (scanned exactly) have no entries.  *n_entries receives the
+ * count; a capacity below it returns UNG_HIP_EINVAL (query/cand/approx may be NULL to
+ * ask for the count).  UNG_HIP_ESTATE when the last call on the context's first
+ * workspace was not a cross-edge call (ung_hip_cross_topk, ung_hip_cross_topk_device,
+ * ung_hip_cross_intra_begin). */
+int ung_hip_debug_partial_rows(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *query, uint32_t *cand, float *approx,
+                               uint64_t *n_entries, double *eps_coef, double *rmax);
+
 /* ---------------------------------------------------------------------------
  * Output boundary (CPU, multi-threaded C++).
  * ------------------------------------------------------------------------- */
