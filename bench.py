@@ -62,11 +62,13 @@ def _sha256_files(paths, extra=b""):
 
 
 def kernel_source_digest():
-    """Digest of what the device code is built from (ung_kernels.hip, which holds every
-    kernel, and the HIP compile flags): a traffic measurement holds while this is
-    unchanged.  Host-side files (ung_runtime.hip, ung_host.cpp) do not enter it."""
+    """Digest of what the select launches are built and planned from: ung_kernels.hip
+    (every kernel), ung_runtime.hip (the work-list planning -- split sizes, item order,
+    partial-row length -- and the launch choices, which change the kernels' traffic) and
+    the HIP compile flags.  A traffic measurement holds while this is unchanged."""
     from filtervectorcode_refactor_amd import build as B
-    return _sha256_files([os.path.join(B.CSRC, "ung_kernels.hip")], " ".join(B.HIP_FLAGS).encode())
+    return _sha256_files([os.path.join(B.CSRC, "ung_kernels.hip"), os.path.join(B.CSRC, "ung_runtime.hip")],
+                         " ".join(B.HIP_FLAGS).encode())
 
 
 def read_traffic(config_name):
@@ -119,6 +121,26 @@ def cpu_model():
     return "unknown"
 
 
+def cpu_inventory():
+    """What the host offers the CPU baseline: logical CPUs of the machine, the ones this
+    process may run on (sched_getaffinity, what `nproc` prints), the OpenMP thread count
+    the environment sets, and the CPU model line."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return {"cpu_model": cpu_model(), "logical_cpus": os.cpu_count(), "nproc": affinity,
+            "omp_num_threads_env": int(omp) if omp and omp.isdigit() else None}
+
+
+def baseline_threads():
+    """Threads of the CPU baseline: OMP_NUM_THREADS when the environment sets it (the GPU
+    box sets the job's CPU share there), else every CPU this process may run on."""
+    inv = cpu_inventory()
+    return inv["omp_num_threads_env"] or inv["nproc"] or inv["logical_cpus"] or 1
+
+
 def _rows_parity(g_ids, g_dist, r_ids, r_dist):
     """(rows, id-exact rows, distance-bit-exact rows) of GPU rows against reference rows."""
     ids_ok = (g_ids == r_ids).all(axis=1)
@@ -142,7 +164,7 @@ def cpu_leg_and_parity(st, cfg, gpu_cross, gpu_intra, p_cross, p_intra, seconds,
     samples compared with its rows.  Returns (cpu_baseline or None, parity)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, RefOracle, ref_available
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = baseline_threads()
     kind = "reference" if ref_available() else "port"
     ref = RefOracle() if kind == "reference" else Oracle()
     k, K = cfg.k_cross, cfg.k_intra
@@ -226,7 +248,9 @@ def cpu_leg_and_parity(st, cfg, gpu_cross, gpu_intra, p_cross, p_intra, seconds,
     else:
         value = r_x
     base = {
-        "value": value, "unit": "distance evals/s", "cores": threads, "kind": kind, "cpu_model": cpu_model(),
+        "value": value, "unit": "distance evals/s", "cores": threads, "kind": kind, **cpu_inventory(),
+        "threads_used": threads,
+        "threads_rule": "OMP_NUM_THREADS when set (the GPU box's CPU share of the job), else nproc",
         "cross_evals_per_s": r_x, "intra_evals_per_s": r_i,
         "sample": f"{q.size} random cross-edge rows of {cfg.name} (exact scan of each row's minimum-superset union, "
                   f"{pairs_x} pairs, {dt_x:.1f} s) and {groups_i} random mid groups ({pairs_i} pairs, {dt_i:.1f} s), "

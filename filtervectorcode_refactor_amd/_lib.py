@@ -44,6 +44,7 @@ class Stats(C.Structure):
         ("fallback_rows", C.c_uint64),
         ("padded_pairs", C.c_uint64),
         ("select_bytes", C.c_uint64),
+        ("allocations", C.c_uint64),
     ]
 
     def as_dict(self) -> dict:
@@ -86,6 +87,7 @@ SIGNATURES = {
     "ung_hip_selftest_mfma": (_int, [_vp, C.POINTER(_dbl)]),
     "ung_hip_debug_partial_rows": (_int, [_vp, _u64, _vp, _vp, _vp, C.POINTER(_u64), C.POINTER(_dbl),
                                           C.POINTER(_dbl)]),
+    "ung_hip_debug_partial_bounds": (_int, [_vp, _u64, _vp, _vp, _vp, _vp, C.POINTER(_u64)]),
     "ung_divide_groups": (_int, [_u64, _vp, _vp, _vp, _vp, _vp, C.POINTER(_u32)]),
     "ung_group_label_sets": (_int, [_u64, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _u64]),
     "ung_lng_build": (_int, [_u32, _vp, _vp, _vp, _vp, _u64, C.POINTER(_u64), _int]),

@@ -39,6 +39,30 @@ static double ms_since(clk::time_point t0)
     return std::chrono::duration<double, std::milli>(clk::now() - t0).count();
 }
 
+// Device (hipMalloc) and pinned host (hipHostMalloc) allocations made by the calling
+// thread; ung_hip_stats::allocations reports the ones made during a call.
+thread_local uint64_t t_alloc_calls = 0;
+
+// Adds the allocations made while it lives to st->allocations (st may be null).
+struct AllocCount {
+    ung_hip_stats *st;
+    uint64_t before;
+    explicit AllocCount(ung_hip_stats *s) : st(s), before(t_alloc_calls) {}
+    ~AllocCount()
+    {
+        if (st)
+            st->allocations += t_alloc_calls - before;
+    }
+    AllocCount(const AllocCount &) = delete;
+    AllocCount &operator=(const AllocCount &) = delete;
+};
+
+hipError_t counted_malloc(void **p, size_t bytes)
+{
+    ++t_alloc_calls;
+    return hipMalloc(p, bytes);
+}
+
 template <class T>
 struct DevBuf {
     T *p = nullptr;
@@ -52,7 +76,7 @@ struct DevBuf {
         p = nullptr;
         cap = 0;
         size_t want = n + n / 4 + 64;
-        hipError_t e = hipMalloc((void **)&p, want * sizeof(T));
+        hipError_t e = counted_malloc((void **)&p, want * sizeof(T));
         if (e != hipSuccess) {
             p = nullptr;
             set_error("hipMalloc(%zu bytes) failed: %s", want * sizeof(T), hipGetErrorString(e));
@@ -83,6 +107,7 @@ struct HostBuf {
         p = nullptr;
         cap = 0;
         const size_t want = n + n / 4 + 4096;
+        ++t_alloc_calls;
         hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
         if (e != hipSuccess) {
             p = nullptr;
@@ -1398,6 +1423,7 @@ int group_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_begin,
         drain_after_failure(ctx);
         return rc;
     }
+    pl.part_lp = pick_lp(list_k, pick_lt(list_k), ctx->d); // partial rows kept for the diagnostics
     if (st)
         st->wall_ms += ms_since(t0);
     return UNG_HIP_OK;
@@ -1625,10 +1651,10 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
     ung_hip_release_vectors(ctx);
     const auto t0 = clk::now();
     const uint32_t dp = (dim + KC - 1) / KC * KC;
-    HIPCHECK(hipMalloc((void **)&ctx->X, N * dim * sizeof(float)));
-    HIPCHECK(hipMalloc((void **)&ctx->XS, N * dp * sizeof(uint32_t)));
-    HIPCHECK(hipMalloc((void **)&ctx->xn, N * sizeof(float)));
-    HIPCHECK(hipMalloc((void **)&ctx->maxbits, sizeof(unsigned int)));
+    HIPCHECK(counted_malloc((void **)&ctx->X, N * dim * sizeof(float)));
+    HIPCHECK(counted_malloc((void **)&ctx->XS, N * dp * sizeof(uint32_t)));
+    HIPCHECK(counted_malloc((void **)&ctx->xn, N * sizeof(float)));
+    HIPCHECK(counted_malloc((void **)&ctx->maxbits, sizeof(unsigned int)));
     HIPCHECK(hipMemcpyAsync(ctx->X, src, N * dim * sizeof(float),
                             src_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream));
     hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(1), dim3(64), 0, ctx->stream, (uint32_t *)ctx->maxbits, 1u);
@@ -1684,6 +1710,9 @@ namespace {
 constexpr int MAX_SCRATCH_DEVICES = 64;
 std::mutex g_scratch_mu;
 unsigned char *g_scratch_addr[MAX_SCRATCH_DEVICES] = {};
+// Held by a no-allocation call for as long as it uses its device's scratch array, so that
+// calls on one GPU from several host threads or contexts run one after the other.
+std::mutex g_scratch_call_mu[MAX_SCRATCH_DEVICES];
 
 // The device address of `scratch` on `device` (current), resolved once per device.
 int resolve_scratch(int device, unsigned char **addr)
@@ -1757,12 +1786,27 @@ int scratch_mem(ung_hip_ctx *ctx, const Plan &pl, uint32_t lp, PlanMem &m)
     return UNG_HIP_OK;
 }
 
-int check_device_ptr(const void *p, int device, const char *what)
+// p must be device memory of `device` with at least `bytes` bytes from p to the end of
+// its allocation (hipMemGetAddressRange), so the kernels' writes stay inside it.
+int check_device_ptr(const void *p, uint64_t bytes, int device, const char *what)
 {
     hipPointerAttribute_t a{};
     if (!p || hipPointerGetAttributes(&a, p) != hipSuccess || a.type != hipMemoryTypeDevice || a.device != device) {
         (void)hipGetLastError();
         set_error("ung_hip_cross_topk_noalloc: %s is not device memory of device %d", what, device);
+        return UNG_HIP_EINVAL;
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, (hipDeviceptr_t)p) != hipSuccess || !base) {
+        (void)hipGetLastError();
+        set_error("ung_hip_cross_topk_noalloc: the allocation holding %s was not found", what);
+        return UNG_HIP_EINVAL;
+    }
+    const uint64_t off = (uint64_t)((const char *)p - (const char *)base);
+    if (off > size || size - off < bytes) {
+        set_error("ung_hip_cross_topk_noalloc: %s has %llu bytes to the end of its allocation, the call writes %llu",
+                  what, (unsigned long long)(off > size ? 0 : size - off), (unsigned long long)bytes);
         return UNG_HIP_EINVAL;
     }
     return UNG_HIP_OK;
@@ -1782,17 +1826,28 @@ int cross_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin, con
         set_error("ung_hip_cross_topk_noalloc: the scratch array of device %d was not resolved", ctx->device);
         return UNG_HIP_ESTATE;
     }
-    if ((rc = set_device(ctx)) || (rc = check_device_ptr(ids, ctx->device, "out_ids_dev")) ||
-        (rc = check_device_ptr(dist, ctx->device, "out_dist_dev")) ||
-        (rc = check_device_ptr(size, ctx->device, "out_size_dev")))
+    if (ctx->device < 0 || ctx->device >= MAX_SCRATCH_DEVICES) {
+        set_error("ung_hip_cross_topk_noalloc: device %d has no scratch array", ctx->device);
+        return UNG_HIP_EINVAL;
+    }
+    const uint64_t row_bytes = ctx->N * k * 4u;
+    if ((rc = set_device(ctx)) || (rc = check_device_ptr(ids, row_bytes, ctx->device, "out_ids_dev")) ||
+        (rc = check_device_ptr(dist, row_bytes, ctx->device, "out_dist_dev")) ||
+        (rc = check_device_ptr(size, ctx->N * 4u, ctx->device, "out_size_dev")))
         return rc;
     const auto t0 = clk::now();
+    // the rows of the context's last allocating cross call are not this call's: the entry
+    // points that describe "the last cross-edge call" refuse until the next such call
+    ctx->cross.valid = false;
+    ctx->cross.rescanned.clear();
     Plan &pl = ctx->plan0;
     plan_reset(pl);
     if ((rc = build_cross_plan(ctx, G, group_begin, out_ptr, out_idx, pl)))
         return rc;
     if (st)
         st->plan_ms += ms_since(t0);
+    // this device's scratch array is this call's until its last kernel has finished
+    std::lock_guard<std::mutex> scratch_lock(g_scratch_call_mu[ctx->device]);
     PlanMem m;
     if ((rc = scratch_mem(ctx, pl, pick_lp(k, pick_lt(k), ctx->d), m)))
         return rc;
@@ -1992,6 +2047,7 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
 int ung_hip_prepare_vectors(ung_hip_ctx *ctx, const float *X, uint64_t N, uint32_t dim, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return prepare_common(ctx, X, false, N, dim, st);
 }
 
@@ -1999,6 +2055,7 @@ int ung_hip_prepare_vectors_device(ung_hip_ctx *ctx, const float *X_dev, uint64_
                                    ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return prepare_common(ctx, X_dev, true, N, dim, st);
 }
 
@@ -2006,6 +2063,7 @@ int ung_hip_cross_topk_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *grou
                               const uint32_t *out_idx, uint32_t k, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return cross_device(ctx, G, group_begin, out_ptr, out_idx, k, st);
 }
 
@@ -2014,6 +2072,7 @@ int ung_hip_cross_topk(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin
                        int32_t *out_size, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     if (!out_ids) {
         set_error("ung_hip_cross_topk: null out_ids");
         return UNG_HIP_EINVAL;
@@ -2033,6 +2092,7 @@ int ung_hip_cross_topk_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *gro
                                int32_t *out_size_dev, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return cross_noalloc(ctx, G, group_begin, out_ptr, out_idx, k, out_ids_dev, out_dist_dev, out_size_dev, st);
 }
 
@@ -2054,6 +2114,7 @@ int ung_hip_download_cross(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist,
                            ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     if (!ctx) {
         set_error("null context");
         return UNG_HIP_EINVAL;
@@ -2066,6 +2127,7 @@ int ung_hip_additional_edges(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group
                              uint32_t *edge_to, uint64_t capacity, uint64_t *n_edges, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return additional_device(ctx, G, group_begin, out_ptr, out_idx, num_cross, edge_ptr, edge_from, edge_to, capacity,
                              n_edges, st);
 }
@@ -2074,6 +2136,7 @@ int ung_hip_group_knn_device(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t
                              const uint32_t *grp_size, uint32_t list_k, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return group_device(ctx, n_groups, grp_begin, grp_size, list_k, st);
 }
 
@@ -2081,6 +2144,7 @@ int ung_hip_group_knn(ung_hip_ctx *ctx, uint32_t n_groups, const uint32_t *grp_b
                       uint32_t list_k, uint32_t *out_ids, float *out_dist, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     if (!out_ids) {
         set_error("ung_hip_group_knn: null out_ids");
         return UNG_HIP_EINVAL;
@@ -2100,12 +2164,14 @@ int ung_hip_cross_intra_begin(ung_hip_ctx *ctx, uint32_t G, const uint32_t *grou
                               const uint32_t *grp_size, uint32_t list_k, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return cross_intra_begin(ctx, G, group_begin, out_ptr, out_idx, k, n_groups, grp_begin, grp_size, list_k, st);
 }
 
 int ung_hip_intra_end(ung_hip_ctx *ctx, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     return intra_end(ctx, st);
 }
 
@@ -2172,6 +2238,7 @@ int ung_hip_rescanned_rows(ung_hip_ctx *ctx, int which, uint32_t *rows, uint64_t
 int ung_hip_download_group(ung_hip_ctx *ctx, uint32_t *out_ids, float *out_dist, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     if (!ctx) {
         set_error("null context");
         return UNG_HIP_EINVAL;
@@ -2184,6 +2251,7 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
                              uint32_t *out_graph, uint32_t *entry_points, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     if (!ctx || !ctx->group.valid) {
         set_error("ung_hip_pack_anchor_rows: run ung_hip_group_knn(_device) first");
         return UNG_HIP_ESTATE;
@@ -2254,6 +2322,7 @@ int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t r
                               float alpha, uint32_t *out_graph, uint32_t *entry_points, ung_hip_stats *st)
 {
     clear_error();
+    AllocCount alloc_count(st);
     if (!ctx || !ctx->group.valid) {
         set_error("ung_hip_prune_group_graph: run ung_hip_group_knn(_device) first");
         return UNG_HIP_ESTATE;
@@ -2365,7 +2434,7 @@ int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err)
     if ((rc = set_device(ctx)))
         return rc;
     float *d_out = nullptr;
-    HIPCHECK(hipMalloc((void **)&d_out, 32 * 32 * sizeof(float)));
+    HIPCHECK(counted_malloc((void **)&d_out, 32 * 32 * sizeof(float)));
     hipLaunchKernelGGL(ung_mfma_probe_kernel, dim3(1), dim3(64), 0, ctx->stream, d_out);
     hipError_t e = hipGetLastError();
     float host[32 * 32];
@@ -2400,7 +2469,7 @@ int ung_hip_debug_partial_rows(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *qu
     }
     const Plan &pl = ctx->plan0;
     if (pl.part_lp == 0) {
-        set_error("ung_hip_debug_partial_rows: no cross call's partial rows on the device");
+        set_error("ung_hip_debug_partial_rows: no partial rows of a cross or synchronous group call on the device");
         return UNG_HIP_ESTATE;
     }
     int rc;
@@ -2450,6 +2519,54 @@ int ung_hip_debug_partial_rows(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *qu
             }
         }
     }
+    return UNG_HIP_OK;
+}
+
+int ung_hip_debug_partial_bounds(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *query, uint32_t *cand_begin,
+                                 uint32_t *cand_end, float *bound, uint64_t *n_rows)
+{
+    clear_error();
+    if (!ctx || !n_rows) {
+        set_error("ung_hip_debug_partial_bounds: null context/n_rows");
+        return UNG_HIP_EINVAL;
+    }
+    const Plan &pl = ctx->plan0;
+    if (pl.part_lp == 0) {
+        set_error("ung_hip_debug_partial_bounds: no partial rows of a cross or synchronous group call on the device");
+        return UNG_HIP_ESTATE;
+    }
+    // rows of the jobs that went through the select (tiny cross jobs have none)
+    uint64_t n = 0;
+    for (const Job &jb : pl.jobs)
+        n += (uint64_t)jb.n_split * jb.q_count;
+    *n_rows = n;
+    if (n > capacity || (n > 0 && (!query || !cand_begin || !cand_end || !bound))) {
+        set_error("ung_hip_debug_partial_bounds: capacity %llu < %llu rows", (unsigned long long)capacity,
+                  (unsigned long long)n);
+        return UNG_HIP_EINVAL;
+    }
+    int rc;
+    if ((rc = set_device(ctx)))
+        return rc;
+    std::vector<float> b(pl.part_rows);
+    if (pl.part_rows)
+        HIPCHECK(hipMemcpyAsync(b.data(), ctx->ws[0].part_bound.p, pl.part_rows * sizeof(float), hipMemcpyDeviceToHost,
+                                ctx->ws[0].stream));
+    HIPCHECK(hipStreamSynchronize(ctx->ws[0].stream));
+    uint64_t r = 0;
+    for (const Job &jb : pl.jobs)
+        for (uint32_t sp = 0; sp < jb.n_split; ++sp) {
+            const uint32_t v0 = sp * jb.split_v;
+            const uint32_t v1 = (uint32_t)std::min<uint64_t>(jb.n_cand, (uint64_t)(sp + 1) * jb.split_v);
+            const bool one = jb.seg_count == 1;
+            const uint32_t s0 = one ? pl.seg_start[jb.seg_begin] : 0u;
+            for (uint32_t qj = 0; qj < jb.q_count; ++qj, ++r) {
+                query[r] = jb.q_begin + qj;
+                cand_begin[r] = one ? s0 + v0 : NONE;
+                cand_end[r] = one ? s0 + v1 : NONE;
+                bound[r] = b[(uint64_t)jb.part_base + (uint64_t)sp * jb.q_count + qj];
+            }
+        }
     return UNG_HIP_OK;
 }
 

@@ -278,6 +278,20 @@ class HipContext:
                                                   C.byref(ec), C.byref(rm)))
         return q, c, a, ec.value, rm.value
 
+    def debug_partial_bounds(self):
+        """(query ids, split candidate ranges [begin, end) as global ids, bounds) of the same
+        call's partial rows (ung_hip_debug_partial_bounds; diagnostic)."""
+        n = C.c_uint64(0)
+        rc = self.lib.ung_hip_debug_partial_bounds(self.h, 0, None, None, None, None, C.byref(n))
+        if rc != 0 and n.value == 0:
+            check(rc)
+        q = np.empty(n.value, np.uint32)
+        b0 = np.empty(n.value, np.uint32)
+        b1 = np.empty(n.value, np.uint32)
+        bd = np.empty(n.value, np.float32)
+        check(self.lib.ung_hip_debug_partial_bounds(self.h, n.value, ptr(q), ptr(b0), ptr(b1), ptr(bd), C.byref(n)))
+        return q, b0, b1, bd
+
 
 # ---------------------------------------------------------------------------
 # host-side inputs (C++ in libung_hip.so)

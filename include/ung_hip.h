@@ -63,6 +63,8 @@ typedef struct ung_hip_stats {
     uint64_t select_bytes;   /* operand bytes the select kernel(s) stream: per work item,
                                 its query rows and its candidate rows of the split base
                                 set (4 * dp bytes a row, dp = dim rounded up to 32) */
+    uint64_t allocations;    /* device (hipMalloc) and pinned host (hipHostMalloc)
+                                allocations the call made (buffers grown on demand) */
 } ung_hip_stats;
 
 /* Message of the calling thread's last failure ("" if none). */
@@ -118,21 +120,26 @@ int ung_hip_cross_result_device(ung_hip_ctx *ctx, uint32_t **ids_dev, float **di
 #define UNG_HIP_NOALLOC_SCRATCH_BYTES (64ull << 20)
 
 /* Cross-group edges that allocate nothing.  No counterpart in the reference: this is for
- * callers that cannot allocate device or pinned memory during the call -- code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same rows as
+ * callers that must not allocate device or pinned memory during the call -- tight serving
+ * loops, harnesses that forbid hipMalloc.  It cannot be captured into a HIP graph: it
+ * plans on the host, uploads from host memory and waits for its own stream.  Same rows as
  * ung_hip_cross_topk_device, written to the caller's device buffers out_ids_dev
  * [N x k], out_dist_dev [N x k] and out_size_dev [N] (all required, device memory of the
- * context's device; checked with hipPointerGetAttributes).  The call's work lists,
- * partial rows and flags live in a file-scope device array of
- * UNG_HIP_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process ends; a call
- * whose plan needs more returns UNG_HIP_EINVAL (the message gives the bytes needed) --
- * roughly 600k result rows with single-split unions at k = 6 and d < 512.  The call makes no
- * hipMalloc, hipHostMalloc or hipFree; its host work lists reuse the context's storage.
- * It needs the base set prepared beforehand (ung_hip_prepare_vectors, which allocates, at
- * set-up).  Every call on one GPU shares that GPU's array: calls that overlap on one GPU
- * (from several host threads or contexts) race.  The rows are not kept in the context
- * (ung_hip_additional_edges does not see them; ung_hip_rescanned_rows does not list
- * them). */
+ * context's device with that many bytes to the end of their allocations; checked with
+ * hipPointerGetAttributes and hipMemGetAddressRange).  The call's work lists, partial rows
+ * and flags live in a file-scope device array of UNG_HIP_NOALLOC_SCRATCH_BYTES (64 MiB)
+ * per GPU, held until the process ends; a call whose plan needs more returns
+ * UNG_HIP_EINVAL (the message gives the bytes needed) -- roughly 600k result rows with
+ * single-split unions at k = 6 and d < 512.  The call makes no hipMalloc, hipHostMalloc
+ * or hipFree (ung_hip_stats::allocations stays 0); its host work lists reuse the
+ * context's storage.  It needs the base set prepared beforehand (ung_hip_prepare_vectors,
+ * which allocates, at set-up).  Calls on one GPU share that GPU's array: a per-device
+ * lock held from the plan's upload to the end of its last kernel makes calls from
+ * several host threads or contexts run one after the other.  The rows are not kept in
+ * the context: afterwards the entry points that read the last cross-edge call's rows
+ * (ung_hip_download_cross, ung_hip_cross_result_device, ung_hip_result_shape(0),
+ * ung_hip_rescanned_rows(0), ung_hip_additional_edges, the diagnostics) return
+ * UNG_HIP_ESTATE until the next allocating cross-edge call. */
 int ung_hip_cross_topk_noalloc(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
                                const uint32_t *out_ptr, const uint32_t *out_idx, uint32_t k,
                                uint32_t *out_ids_dev, float *out_dist_dev, int32_t *out_size_dev,
@@ -264,17 +271,29 @@ int ung_hip_synchronize(ung_hip_ctx *ctx);
 int ung_hip_selftest_mfma(ung_hip_ctx *ctx, double *max_abs_err);
 
 /* Diagnostic, no counterpart in the reference: the approximate (split-bf16 MFMA,
- * expansion-form) distances behind the context's last cross-edge call, for checking the
+ * expansion-form) distances behind the context's last cross-edge call or synchronous
+ * group kNN call (ung_hip_group_knn, ung_hip_group_knn_device), for checking the
  * certified error bound against exact distances.  Writes one entry per partial-row
  * candidate -- query id, candidate id (global ids), approximate squared distance a --
  * and the bound's constants: |a - D| <= eps_coef * (|q| + rmax)^2 for the exact squared
  * distance D.  Tiny jobs (scanned exactly) have no entries.  *n_entries receives the
  * count; a capacity below it returns UNG_HIP_EINVAL (query/cand/approx may be NULL to
  * ask for the count).  UNG_HIP_ESTATE when the last call on the context's first
- * workspace was not a cross-edge call (ung_hip_cross_topk, ung_hip_cross_topk_device,
- * ung_hip_cross_intra_begin). */
+ * workspace was neither of those (ung_hip_cross_topk, ung_hip_cross_topk_device,
+ * ung_hip_cross_intra_begin, ung_hip_group_knn, ung_hip_group_knn_device). */
 int ung_hip_debug_partial_rows(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *query, uint32_t *cand, float *approx,
                                uint64_t *n_entries, double *eps_coef, double *rmax);
+
+/* Diagnostic, no counterpart in the reference: the bound of every partial row of the same
+ * call (the select's contract: every candidate of the row's split that the row does not
+ * hold has an approximate distance a >= bound, so an exact distance D >= bound -
+ * eps_coef * (|q| + rmax)^2).  One row per (query, split): query id, the split's
+ * candidates as the global id range [cand_begin, cand_end) when the job's union is one
+ * range (every group kNN job; UINT32_MAX for multi-range cross unions), and the bound
+ * (+inf: the split holds no candidate past the row).  *n_rows receives the count; a
+ * capacity below it returns UNG_HIP_EINVAL.  UNG_HIP_ESTATE as above. */
+int ung_hip_debug_partial_bounds(ung_hip_ctx *ctx, uint64_t capacity, uint32_t *query, uint32_t *cand_begin,
+                                 uint32_t *cand_end, float *bound, uint64_t *n_rows);
 
 /* ---------------------------------------------------------------------------
  * Output boundary (CPU, multi-threaded C++).

@@ -85,6 +85,19 @@ def test_lng_order_matches_reference_trie(ref_oracle, name, n):
     assert np.array_equal(op, rop) and np.array_equal(oi, roi)
 
 
+@pytest.mark.parametrize("name", ["cfg2", "cfg4", "cfg5"])
+def test_lng_order_full_scale(ref_oracle, name):
+    """The full configurations' labels (cfg2: 30,883 groups and 109,476 LNG entries; cfg5:
+    10M vectors, 63,542 groups, 241,680 entries): groups and LNG rows element by element,
+    order included, against the reference's TrieIndex.  (cfg3's 187,608 groups take the
+    reference's trie over two minutes; its order is pinned on samples above.)"""
+    lp, li = D.synth_labels(D.CONFIGS[name])
+    G, pg, _, op, oi = _lng_of(lp, li, nthreads=8)
+    rG, rpg, rop, roi = ref_oracle.trie_lng(lp, li)
+    assert G == rG and np.array_equal(pg, rpg)
+    assert np.array_equal(op, rop) and np.array_equal(oi, roi)
+
+
 @pytest.mark.parametrize("seed,vocab,mmax,lo,offset", [(11, 5, 4, 0, 0), (12, 40, 8, 0, 0), (13, 200, 3, 1, 0),
                                                        (14, 12, 6, 0, 5000), (15, 3, 3, 0, 0), (16, 64, 5, 1, 60)])
 def test_lng_order_random_families(ref_oracle, seed, vocab, mmax, lo, offset):
@@ -185,6 +198,33 @@ def test_formats_roundtrip(tmp_path):
     assert np.array_equal(lp, lp2) and np.array_equal(li, li2)
     lp3, li3 = D.read_labels(os.path.join(tmp_path, "missing.txt"), 4)
     assert lp3.tolist() == [0, 1, 2, 3, 4] and li3.tolist() == [1, 1, 1, 1]
+
+
+# Group sizes around every boundary of the size router, and the groups each route gets,
+# worked out by hand from partition_tagore_groups (src/uni_nav_graph_group_graph.cpp:
+# 625-641: n <= complete_threshold or n < tagore_min_group_size -> CPU fallback),
+# make_tagore_group_graph_settings (src/ung_build_settings.cpp:232-237: complete_threshold
+# = max(max_degree, 64)) and build_tagore_batch_artifacts (:656-677: n <=
+# exact_batch_threshold = 4096 -> exact batch, else the large-group batch), with
+# tagore_min_group_size = 128.
+ROUTER_SIZES = [1, 2, 63, 64, 65, 100, 127, 128, 129, 199, 200, 201, 4095, 4096, 4097, 70000]
+ROUTER_EXPECT = {
+    # max_degree: (mid-group sizes, large-group sizes)
+    32: ([128, 129, 199, 200, 201, 4095, 4096], [4097, 70000]),
+    128: ([129, 199, 200, 201, 4095, 4096], [4097, 70000]),     # n = 128 is complete
+    200: ([201, 4095, 4096], [4097, 70000]),                    # n <= 200 complete
+    5000: ([], [70000]),                                        # n <= 5000 complete
+}
+
+
+@pytest.mark.parametrize("max_degree", sorted(ROUTER_EXPECT))
+def test_size_router_boundaries(max_degree):
+    st = F.UngBuildStage(max_degree=max_degree)
+    st.group_begin = np.concatenate([[0, 0], np.cumsum(ROUTER_SIZES)]).astype(np.uint32)
+    sizes = np.array(ROUTER_SIZES)
+    mids, large = ROUTER_EXPECT[max_degree]
+    assert sizes[st.mid_groups().astype(np.int64) - 1].tolist() == mids
+    assert sizes[st.large_groups().astype(np.int64) - 1].tolist() == large
 
 
 def test_stage_mid_groups_router(cfg1_stage):
