@@ -343,10 +343,26 @@ def main():
     ms_per_step = wall * 1e3 / steps
     log(f"{steps} timed steps: {ms_per_step:.3f} ms/step")
 
-    # the drop-in calls with host output (D2H included), after the timed region
+    # the drop-in calls with host output (D2H included), after the timed region: the cross
+    # rows with distances and sizes, the FlatId rows alone (the reference's flat writeback,
+    # src/gpu_cross_edge_output.cuh:87-103), the exact batch's packed rows [P x (K+1)]
+    # (what build_fast_exact_cuda_batch hands to fill_tagore_batch_results,
+    # src/tagore_graph_builder.cu:1354-1379) and the exact lists with distances
     dropin = [ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross) for _ in range(3)]
     g_cross = (dropin[-1][0], dropin[-1][1])
     cross_rescanned = int(dropin[-1][3]["fallback_rows"])
+    flat_dropin = [ctx.cross_topk(st.group_begin, st.out_ptr, st.out_idx, cfg.k_cross, with_dist=False,
+                                  with_size=False)[3] for _ in range(3)]
+    fd = cfg.k_intra
+    tk, head_keep = max(st.tagore_k, fd + 1), (fd - 8 if fd > 8 else fd)
+
+    def exact_batch():
+        t0 = time.perf_counter()
+        s_knn = ctx.group_knn_device(begins, sizes, fd)
+        graph, _, s_pack = ctx.pack_anchor_rows(int(sizes.sum()), len(gids), tk, fd, head_keep, 1, 0, 0)
+        return (time.perf_counter() - t0) * 1e3, s_knn, s_pack, graph
+
+    packed_dropin = [exact_batch() for _ in range(3)]
     intra_dropin = [ctx.group_knn(begins, sizes, cfg.k_intra) for _ in range(2)]
     g_intra = (intra_dropin[-1][0], intra_dropin[-1][1], gids, begins, sizes)
     intra_rescanned = int(intra_dropin[-1][2]["fallback_rows"])
@@ -426,11 +442,20 @@ def main():
             "resident_upload_ms": round(up["h2d_ms"], 3),
             "cross_dropin_wall_ms": round(float(np.mean([s[3]["wall_ms"] for s in dropin])), 3),
             "cross_dropin_d2h_ms": round(float(np.mean([s[3]["d2h_ms"] for s in dropin])), 3),
+            "cross_flat_dropin_wall_ms": round(float(np.mean([s["wall_ms"] for s in flat_dropin])), 3),
+            "cross_flat_dropin_d2h_ms": round(float(np.mean([s["d2h_ms"] for s in flat_dropin])), 3),
+            "exact_batch_packed_dropin_wall_ms": round(float(np.mean([x[0] for x in packed_dropin])), 3),
+            "exact_batch_packed_d2h_ms": round(float(np.mean([x[2]["d2h_ms"] for x in packed_dropin])), 3),
+            "exact_batch_packed_bytes": int(packed_dropin[-1][3].nbytes),
             "intra_dropin_wall_ms": round(float(np.mean([s[2]["wall_ms"] for s in intra_dropin])), 3),
             "intra_dropin_d2h_ms": round(float(np.mean([s[2]["d2h_ms"] for s in intra_dropin])), 3),
-            "dropin_note": "ung_hip_cross_topk / ung_hip_group_knn with host output (FlatId rows + distances + "
-                           "sizes, D2H included), run after the timed steps; the one-time upload of X is "
-                           "resident_upload_ms",
+            "dropin_note": "host-output calls after the timed steps, D2H included (pinned staging, pieces copied "
+                           "to the caller's memory on the host threads while the next ones transfer): "
+                           "cross_dropin = ung_hip_cross_topk with FlatId rows + distances + sizes; "
+                           "cross_flat_dropin = the FlatId rows alone; exact_batch_packed_dropin = "
+                           "ung_hip_group_knn_device + ung_hip_pack_anchor_rows with the packed rows "
+                           f"[P x {fd + 1}] u32 on the host; intra_dropin = ung_hip_group_knn lists + distances; "
+                           "the one-time upload of X is resident_upload_ms",
         },
     }
     log("cpu baseline + parity ..." if not args.no_cpu_baseline else "parity ...")

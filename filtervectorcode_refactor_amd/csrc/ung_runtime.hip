@@ -13,7 +13,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "ung_hip.h"
@@ -315,6 +317,10 @@ struct ung_hip_ctx {
     DevBuf<unsigned long long> a_cnt;
     DevBuf<unsigned char> a_tmp;
     HostBuf a_stage;
+    // result downloads to host memory: DL_SLOTS pinned staging slots of DL_PIECE bytes and
+    // an event per slot (see download_regions)
+    HostBuf dl_stage;
+    std::vector<hipEvent_t> dl_ev; // one per piece of the largest download so far
     // host threads of the work-list planning and staging (persistent, created at create)
     std::unique_ptr<ung::WorkerPool> pool;
     // test hook: UNG_HIP_FORCE_WIDE=1 at create selects the > 4 GiB load mode for any size
@@ -1614,6 +1620,115 @@ int additional_device(ung_hip_ctx *ctx, uint32_t G, const uint32_t *group_begin,
     return UNG_HIP_OK;
 }
 
+// Device-to-host copy of result regions into the caller's (pageable) memory through the
+// context's pinned staging: the regions are cut into pieces of DL_PIECE bytes that cycle
+// through DL_SLOTS pinned slots.  One run of the worker pool does all host copies: worker
+// t copies part t of every piece in order (waiting for the piece's DMA event), and the
+// worker that finishes a piece's last part enqueues the DMA of the piece that reuses its
+// slot.  So the DMA engine fills the next slots while the host threads copy the finished
+// piece into the caller's memory (first-touch page faults of a fresh destination
+// included), and the transfer runs near the link's pinned rate instead of the runtime's
+// single-threaded pageable path.  Small copies go straight through.
+constexpr size_t DL_PIECE = 8u << 20;
+constexpr int DL_SLOTS = 4;
+constexpr size_t DL_DIRECT = 1u << 20; // below this, one plain copy
+
+struct DlRegion {
+    void *dst;
+    const void *src;
+    size_t bytes;
+};
+
+int download_regions(ung_hip_ctx *ctx, hipStream_t stream, const DlRegion *reg, int nreg)
+{
+    size_t total = 0;
+    for (int r = 0; r < nreg; ++r)
+        total += reg[r].dst ? reg[r].bytes : 0;
+    if (total < DL_DIRECT || !ctx->pool || ctx->pool->size() < 2) {
+        for (int r = 0; r < nreg; ++r)
+            if (reg[r].dst && reg[r].bytes)
+                HIPCHECK(hipMemcpyAsync(reg[r].dst, reg[r].src, reg[r].bytes, hipMemcpyDeviceToHost, stream));
+        HIPCHECK(hipStreamSynchronize(stream));
+        return UNG_HIP_OK;
+    }
+    int rc;
+    if ((rc = ctx->dl_stage.ensure(DL_PIECE * DL_SLOTS)))
+        return rc;
+    struct Piece {
+        char *dst;
+        const char *src;
+        size_t bytes;
+    };
+    std::vector<Piece> pieces;
+    for (int r = 0; r < nreg; ++r) {
+        if (!reg[r].dst)
+            continue;
+        for (size_t o = 0; o < reg[r].bytes; o += DL_PIECE)
+            pieces.push_back(Piece{static_cast<char *>(reg[r].dst) + o, static_cast<const char *>(reg[r].src) + o,
+                                   std::min(DL_PIECE, reg[r].bytes - o)});
+    }
+    const size_t np = pieces.size();
+    while (ctx->dl_ev.size() < np) {
+        hipEvent_t ev = nullptr;
+        HIPCHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        ctx->dl_ev.push_back(ev);
+    }
+    char *stage = static_cast<char *>(ctx->dl_stage.p);
+    // enqueue[i]: DMA of piece i into its slot and its event (the event is recorded before
+    // the flag is raised, so a worker that sees the flag waits on this piece's DMA)
+    std::unique_ptr<std::atomic<int>[]> queued(new std::atomic<int>[np]);
+    std::unique_ptr<std::atomic<int>[]> done(new std::atomic<int>[np]);
+    for (size_t i = 0; i < np; ++i) {
+        queued[i].store(0, std::memory_order_relaxed);
+        done[i].store(0, std::memory_order_relaxed);
+    }
+    std::atomic<int> failed{0};
+    auto enqueue = [&](size_t i) -> int {
+        const size_t slot = i % DL_SLOTS;
+        if (hipMemcpyAsync(stage + slot * DL_PIECE, pieces[i].src, pieces[i].bytes, hipMemcpyDeviceToHost, stream) !=
+                hipSuccess ||
+            hipEventRecord(ctx->dl_ev[i], stream) != hipSuccess)
+            return UNG_HIP_EDEVICE;
+        queued[i].store(1, std::memory_order_release);
+        return UNG_HIP_OK;
+    };
+    for (size_t i = 0; i < np && i < (size_t)DL_SLOTS; ++i)
+        if (enqueue(i) != UNG_HIP_OK) {
+            (void)hipStreamSynchronize(stream);
+            set_error("download: device-to-host copy failed");
+            return UNG_HIP_EDEVICE;
+        }
+    const int T = ctx->pool->size();
+    const int device = ctx->device;
+    ctx->pool->run(T, [&](int64_t t) {
+        (void)hipSetDevice(device);
+        for (size_t i = 0; i < np; ++i) {
+            while (!queued[i].load(std::memory_order_acquire)) {
+                if (failed.load(std::memory_order_relaxed))
+                    return;
+                std::this_thread::yield();
+            }
+            if (hipEventSynchronize(ctx->dl_ev[i]) != hipSuccess) {
+                failed.store(1);
+                return;
+            }
+            const Piece &pc = pieces[i];
+            const size_t b0 = pc.bytes * (size_t)t / (size_t)T, b1 = pc.bytes * (size_t)(t + 1) / (size_t)T;
+            std::memcpy(pc.dst + b0, stage + (i % DL_SLOTS) * DL_PIECE + b0, b1 - b0);
+            // the last part of piece i frees its slot for piece i + DL_SLOTS
+            if (done[i].fetch_add(1, std::memory_order_acq_rel) == T - 1 && i + DL_SLOTS < np &&
+                enqueue(i + DL_SLOTS) != UNG_HIP_OK)
+                failed.store(1);
+        }
+    });
+    if (failed.load()) {
+        (void)hipStreamSynchronize(stream);
+        set_error("download: device-to-host copy failed");
+        return UNG_HIP_EDEVICE;
+    }
+    return UNG_HIP_OK;
+}
+
 int download(ung_hip_ctx *ctx, ResultBufs &res, uint32_t *ids, float *dist, int32_t *size, ung_hip_stats *st)
 {
     if (!res.valid) {
@@ -1626,14 +1741,12 @@ int download(ung_hip_ctx *ctx, ResultBufs &res, uint32_t *ids, float *dist, int3
     }
     const auto t0 = clk::now();
     const size_t n = (size_t)res.rows * res.k;
-    if (n) {
-        HIPCHECK(hipMemcpyAsync(ids, res.ids.p, n * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
-        if (dist)
-            HIPCHECK(hipMemcpyAsync(dist, res.dist.p, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
-        if (size)
-            HIPCHECK(hipMemcpyAsync(size, res.size.p, res.rows * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
-    }
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    const DlRegion reg[3] = {{ids, res.ids.p, n * sizeof(uint32_t)},
+                             {dist, res.dist.p, n * sizeof(float)},
+                             {size, res.size.p, (size_t)res.rows * sizeof(int32_t)}};
+    int rc;
+    if ((rc = download_regions(ctx, ctx->stream, reg, 3)))
+        return rc;
     if (st)
         st->d2h_ms += ms_since(t0);
     return UNG_HIP_OK;
@@ -1676,6 +1789,10 @@ int prepare_common(ung_hip_ctx *ctx, const float *src, bool src_device, uint64_t
     HIPCHECK(hipStreamSynchronize(ctx->stream));
     float mxf;
     std::memcpy(&mxf, &mb, sizeof(mxf));
+    // the pinned staging of result downloads, once per context at set-up (not in the
+    // first download's time)
+    if ((rc = ctx->dl_stage.ensure(DL_PIECE * DL_SLOTS)))
+        return rc;
     ctx->N = N;
     ctx->d = dim;
     ctx->dp = dp;
@@ -2026,6 +2143,11 @@ int ung_hip_destroy(ung_hip_ctx *ctx)
     ctx->a_cnt.release();
     ctx->a_tmp.release();
     ctx->a_stage.release();
+    ctx->dl_stage.release();
+    for (hipEvent_t ev : ctx->dl_ev)
+        if (ev)
+            (void)hipEventDestroy(ev);
+    ctx->dl_ev.clear();
     for (auto &ev : ctx->ev)
         if (ev)
             (void)hipEventDestroy(ev);
@@ -2302,9 +2424,9 @@ int ung_hip_pack_anchor_rows(ung_hip_ctx *ctx, uint32_t tagore_k, uint32_t final
         HIPCHECK(hipEventRecord(ctx->ev[7], ctx->stream));
     }
     const auto t1 = clk::now();
-    if (rows)
-        HIPCHECK(hipMemcpyAsync(out_graph, ctx->graph.p, rows * stride * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    const DlRegion reg{out_graph, ctx->graph.p, (size_t)rows * stride * sizeof(uint32_t)};
+    if ((rc = download_regions(ctx, ctx->stream, &reg, 1)))
+        return rc;
     if (entry_points)
         std::memset(entry_points, 0, ctx->group_jobs.size() * sizeof(uint32_t));
     if (st) {
@@ -2396,8 +2518,9 @@ int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t r
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipEventRecord(ctx->ev[7], ctx->stream));
     const auto t1 = clk::now();
-    HIPCHECK(hipMemcpyAsync(out_graph, ctx->graph.p, rows * stride * sizeof(uint32_t), hipMemcpyDeviceToHost, ctx->stream));
-    HIPCHECK(hipStreamSynchronize(ctx->stream));
+    const DlRegion reg{out_graph, ctx->graph.p, (size_t)rows * stride * sizeof(uint32_t)};
+    if ((rc = download_regions(ctx, ctx->stream, &reg, 1)))
+        return rc;
     // FastGrnnd's entry point is the group's first point (ep_dev cleared, :2036)
     if (entry_points)
         std::memset(entry_points, 0, n_jobs * sizeof(uint32_t));

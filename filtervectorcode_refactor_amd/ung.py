@@ -85,14 +85,16 @@ class HipContext:
     def release_vectors(self):
         check(self.lib.ung_hip_release_vectors(self.h))
 
-    def cross_topk(self, group_begin, out_ptr, out_idx, k: int, with_dist=True):
+    def cross_topk(self, group_begin, out_ptr, out_idx, k: int, with_dist=True, with_size=True):
+        """Cross edges with host output (ung_hip_cross_topk): ids [N x k] (the FlatId rows),
+        distances and row sizes when asked for (None otherwise), stats."""
         group_begin, out_ptr = u32(group_begin), u32(out_ptr)
         out_idx = u32(out_idx) if len(out_idx) else np.zeros(1, np.uint32)
         G = group_begin.shape[0] - 2
         N = int(group_begin[-1])
         ids = np.empty((N, k), np.uint32)
         dist = np.empty((N, k), np.float32) if with_dist else None
-        size = np.empty(N, np.int32)
+        size = np.empty(N, np.int32) if with_size else None
         st = Stats()
         check(self.lib.ung_hip_cross_topk(self.h, G, ptr(group_begin), ptr(out_ptr), ptr(out_idx), k,
                                           ptr(ids), ptr(dist), ptr(size), C.byref(st)))

@@ -8,10 +8,12 @@
 // Paths are relative to UNG/codes/ of panjd123/FilterVectorCode_refactor.
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
 #include <limits>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <utility>
 #include <vector>
 
@@ -92,28 +94,50 @@ class Backend {
         }
         const uint64_t N = group_begin[G + 1];
         k_ = (uint32_t)topk;
-        ids_.assign(N * k_, 0);
-        dists_.assign(N * k_, 0.0f);
-        sizes_.assign(N, 0);
-        throw_if(ung_hip_cross_topk(ctx_, G, group_begin.data(), out_ptr.data(), out_idx.empty() ? nullptr : out_idx.data(),
-                                    k_, ids_.data(), dists_.data(), sizes_.data(), &last_),
+        last_ = ung_hip_stats{};
+        throw_if(ung_hip_cross_topk_device(ctx_, G, group_begin.data(), out_ptr.data(),
+                                           out_idx.empty() ? nullptr : out_idx.data(), k_, &last_),
                  "cross_groups_search_all_batched");
-        if (flat_ids)
-            *flat_ids = ids_;
+        // the rows go straight into the caller's vectors (no second host copy): ids into
+        // flat_ids when given (else the adapter's own buffer), distances into flat_dists;
+        // for_each_cross_edge fetches ids and distances again when it needs them
+        have_rows_ = false;
+        sizes_.resize(N);
+        std::vector<uint32_t> *ids = flat_ids ? flat_ids : &ids_;
+        ids->resize(N * k_);
         if (flat_dists)
-            *flat_dists = dists_;
+            flat_dists->resize(N * k_);
+        throw_if(ung_hip_download_cross(ctx_, ids->data(), flat_dists ? flat_dists->data() : nullptr, sizes_.data(),
+                                        &last_),
+                 "cross_groups_search_all_batched (download)");
         if (id_vectors) {
+            // IdVector writeback, rows filled in parallel
             id_vectors->assign(N, {});
-            for (uint64_t p = 0; p < N; ++p)
-                (*id_vectors)[p].assign(ids_.begin() + p * k_, ids_.begin() + p * k_ + sizes_[p]);
+            const uint32_t *src = ids->data();
+            const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+            std::vector<std::thread> pool;
+            for (unsigned t = 0; t < nt; ++t)
+                pool.emplace_back([&, t] {
+                    for (uint64_t p = N * t / nt; p < N * (t + 1) / nt; ++p)
+                        (*id_vectors)[p].assign(src + p * k_, src + p * k_ + sizes_[p]);
+                });
+            for (auto &th : pool)
+                th.join();
         }
     }
 
     // SearchQueue writeback: sink(point, id, dist) for every cross edge, in
     // (dist, id) order per point -- e.g. [&](auto p, auto id, auto d){ queues[p].insert(id, d); }.
+    // Reads the rows of the last cross_groups_search_all_batched call from the device.
     template <class Sink>
-    void for_each_cross_edge(Sink &&sink) const
+    void for_each_cross_edge(Sink &&sink)
     {
+        if (!have_rows_) {
+            ids_.resize(sizes_.size() * k_);
+            dists_.resize(sizes_.size() * k_);
+            throw_if(ung_hip_download_cross(ctx_, ids_.data(), dists_.data(), nullptr, &last_), "for_each_cross_edge");
+            have_rows_ = true;
+        }
         for (uint64_t p = 0; p < sizes_.size(); ++p)
             for (int32_t j = 0; j < sizes_[p]; ++j)
                 sink((uint32_t)p, ids_[p * k_ + j], dists_[p * k_ + j]);
@@ -239,6 +263,7 @@ class Backend {
     std::vector<uint32_t> ids_;
     std::vector<float> dists_;
     std::vector<int32_t> sizes_;
+    bool have_rows_ = false; // ids_/dists_ hold the last search's rows
 };
 
 } // namespace ung_hip
