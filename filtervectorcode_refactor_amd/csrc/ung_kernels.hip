@@ -3084,6 +3084,12 @@ struct PruneParams {
     uint32_t *rev_src;    // [total] source local ids
     float *rev_dist;
     uint32_t *graph;      // [rows x (final_degree + 1)]
+    // the certified Gram pre-decision (ung_prune_gram_kernel)
+    const uint32_t *xs;   // split base set, [N][dp] words
+    const float *xn;      // squared norms
+    uint32_t dp;
+    double eps_coef;      // expansion-form error factor (as the select's), on (|a| + |b|)^2
+    double shrink;        // relative error of the reference summation
 };
 
 // Job (group) of a result row: the last job whose first row is <= r.
@@ -3225,6 +3231,240 @@ __global__ __launch_bounds__(64) void ung_prune_kernel(PruneParams K)
         row[0] = na;
     for (uint32_t j = (uint32_t)lane; j < K.final_degree; j += 64)
         row[1 + j] = j < na ? kept[j] : s;
+}
+
+// ---------------------------------------------------------------------------
+// The same prune with its alpha tests decided from a certified Gram matrix: the row's
+// candidates (at most 96: forward_cap <= 64 plus reverse_cap <= 32) go through the split-bf16
+// MFMA passes of the select kernel as a 96 x 96 Gram matrix (upper triangle: six 32 x 32
+// blocks), so an approximate distance of every pair of candidates costs no row loads of its
+// own.  The alpha test `alpha * d(kept, cand) < d(row, cand)` of the exact scan
+// (fp32 distances in the reference's summation order) is then decided from bounds: with
+// D~ = |a|^2 + |b|^2 - 2 G(a, b) and |D~ - D| <= eps_coef (|a| + |b|)^2 (the select's error
+// model: split operands, accumulation from 0, norm caches and the final fma), the
+// reference's distance lies in [L, U] = lower_bound_ea / upper_bound_ea of D~; fp32
+// multiplication by alpha is monotone, so fl(alpha U) < d(row, cand) proves a rejection and
+// fl(alpha L) >= d(row, cand) proves a pass.  Only pairs left undecided (near the
+// boundary, or exact ties) are scored exactly, as in ung_prune_kernel.  The kept lists are
+// therefore identical to ung_prune_kernel's.  One wave per row.
+// ---------------------------------------------------------------------------
+constexpr int PG_N = 96;             // candidates of a row (padded)
+constexpr int PG_W = KC + 4;         // staged chunk row stride (words)
+
+// Block (bi, bj), bi <= bj, of the upper triangle of 32 x 32 blocks: 0 1 2 / 3 4 / 5.
+__device__ __forceinline__ int pg_block(int bi, int bj)
+{
+    return bj + (bi == 0 ? 0 : bi + 1);
+}
+
+struct alignas(16) PruneGramSmem {
+    union {
+        float4 xs[2][PG_N][PG_W / 4]; // a chunk (32 dimensions) of every candidate row, two
+                                      // buffers
+        float g[6][32][33];           // the Gram blocks after the last chunk (pg_block order)
+    } u;
+    float cd[128];
+    uint32_t ci[128];
+    float cn[PG_N];                  // candidates' squared norms
+    float cr[PG_N];                  // and norms (rounded up)
+    float rd[32];
+    uint32_t ri[32];
+    uint32_t kept[64];               // kept candidates (local ids)
+    uint32_t kpos[64];               // and their positions in the candidate list
+    uint32_t ncand;
+};
+
+__global__ __launch_bounds__(64) void ung_prune_gram_kernel(PruneParams K)
+{
+    __shared__ PruneGramSmem sm;
+    const int lane = threadIdx.x;
+    const uint64_t r = blockIdx.x;
+    if (r >= K.rows)
+        return;
+    const Job jb = K.jobs[job_of_row(K.jobs, K.n_jobs, (uint32_t)r)];
+    const uint32_t s = (uint32_t)r - jb.out_row;
+    const uint32_t cnt_f = min((uint32_t)K.size[r], K.forward_cap);
+    // the reverse_cap nearest reverse edges (as ung_prune_kernel)
+    const uint32_t r0 = K.rev_cnt[r], r1 = K.rev_cnt[r + 1];
+    float bd = INFINITY;
+    uint32_t bi = NONE;
+    for (uint32_t c0 = r0; c0 < r1; c0 += 32) {
+        if (lane >= 32) {
+            const uint32_t at = c0 + (uint32_t)(lane - 32);
+            bd = at < r1 ? K.rev_dist[at] : INFINITY;
+            bi = at < r1 ? K.rev_src[at] : NONE;
+        }
+        wave_sort64(bd, bi, lane);
+    }
+    const uint32_t cnt_r = min(K.reverse_cap, r1 - r0);
+    if ((uint32_t)lane < cnt_r) {
+        sm.rd[lane] = bd;
+        sm.ri[lane] = bi;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        const float *fdp = K.dist + r * K.list_k;
+        const uint32_t *fip = K.ids + r * K.list_k;
+        uint32_t i = 0, j = 0, nc = 0;
+        while (i < cnt_f || j < cnt_r) {
+            const bool take_f = j == cnt_r || (i < cnt_f && !cand_less(sm.rd[j], sm.ri[j], fdp[i], fip[i]));
+            const float dv = take_f ? fdp[i] : sm.rd[j];
+            const uint32_t iv = take_f ? fip[i] : sm.ri[j];
+            i += take_f ? 1u : 0u;
+            j += take_f ? 0u : 1u;
+            if (nc > 0 && sm.ci[nc - 1] == iv)
+                continue; // the same id twice carries the same distance: adjacent
+            sm.cd[nc] = dv;
+            sm.ci[nc] = iv;
+            ++nc;
+        }
+        sm.ncand = nc;
+    }
+    __syncthreads();
+    const uint32_t nc = sm.ncand; // <= cnt_f + cnt_r <= 96
+    const float *__restrict__ X = K.X + (size_t)jb.q_begin * K.d;
+    const uint32_t *__restrict__ XS = K.xs + (size_t)jb.q_begin * K.dp;
+    // padding positions (>= nc) repeat the row's own point: their Gram entries are never read
+    for (uint32_t i = (uint32_t)lane; i < (uint32_t)PG_N; i += 64u) {
+        const float x2 = i < nc ? K.xn[jb.q_begin + sm.ci[i]] : 0.0f;
+        sm.cn[i] = x2;
+        sm.cr[i] = __double2float_ru(sqrt((double)fmaxf(x2, 0.0f) * (1.0 + 1e-6)));
+    }
+
+    // Gram of the candidates: chunk by chunk (32 dimensions = two k-blocks of 16) through
+    // LDS; lane (r32, h) feeds row/column r32 of a 32-block, dimensions 16 kb + 8 h .. + 7;
+    // three passes per k-block (hi*hi, hi*lo, lo*hi), blocks (bi, bj) with bi <= bj
+    const int r32 = lane & 31, h = lane >> 5;
+    floatx16 acc[6];
+    const floatx16 zero = {};
+    // loader: row lr = lane / 8 + 8 m (m = 0..11), float4 column c4 = lane % 8 of the chunk
+    const int lc = lane & 7, lr0 = lane >> 3;
+    const uint32_t nk = K.dp / KC;
+    // the lane's rows (local ids)
+    uint32_t rid[PG_N / 8];
+#pragma unroll
+    for (int m = 0; m < PG_N / 8; ++m) {
+        const uint32_t row = (uint32_t)(lr0 + 8 * m);
+        rid[m] = row < nc ? sm.ci[row] : s;
+    }
+    const uint32_t *__restrict__ XSl = XS + 4u * (uint32_t)lc;
+    // chunk kc + 1 is loaded into registers while chunk kc is multiplied from LDS, and
+    // staged into the other LDS buffer after it
+    u32x4 pre[PG_N / 8];
+    auto load_chunk = [&](uint32_t kc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < PG_N / 8; ++m)
+            pre[m] = *reinterpret_cast<const u32x4 *>(XSl + (size_t)rid[m] * K.dp + kc * KC);
+    };
+    auto stage_chunk = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < PG_N / 8; ++m)
+            *reinterpret_cast<u32x4 *>(&sm.u.xs[buf][lr0 + 8 * m][lc]) = pre[m];
+    };
+    load_chunk(0);
+    stage_chunk(0);
+    __syncthreads();
+    if (nk > 1)
+        load_chunk(1);
+    for (uint32_t kc = 0; kc < nk; ++kc) {
+        const int buf = (int)(kc & 1u);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const int ch = 2 * kb + h;
+            bf16x8 hi[3], lo[3];
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                hi[b] = __builtin_bit_cast(bf16x8, sm.u.xs[buf][32 * b + r32][ch]);
+                lo[b] = __builtin_bit_cast(bf16x8, sm.u.xs[buf][32 * b + r32][ch + 4]);
+            }
+            // pass-major: six independent accumulators between dependent MFMAs
+            const bool z = kc == 0 && kb == 0;
+            constexpr int BI[6] = {0, 0, 0, 1, 1, 2}, BJ[6] = {0, 1, 2, 1, 2, 2}; // pg_block order
+#pragma unroll
+            for (int t = 0; t < 6; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi[BI[t]], hi[BJ[t]], z ? zero : acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 6; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi[BI[t]], lo[BJ[t]], acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 6; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo[BI[t]], hi[BJ[t]], acc[t], 0, 0, 0);
+        }
+        if (kc + 1 < nk)
+            stage_chunk(buf ^ 1); // its previous reads (chunk kc - 1) ended at the last barrier
+        __syncthreads();
+        if (kc + 2 < nk)
+            load_chunk(kc + 2);
+    }
+    // (the loop's last barrier ended the last chunk's operand reads: the Gram takes their
+    // place)
+    {
+        int t = 0;
+#pragma unroll
+        for (int bi2 = 0; bi2 < 3; ++bi2)
+#pragma unroll
+            for (int bj = bi2; bj < 3; ++bj, ++t)
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    sm.u.g[t][8 * (q >> 2) + 4 * h + (q & 3)][r32] = acc[t][q];
+    }
+    __syncthreads();
+
+    // greedy scan: lane l < na holds kept point l; a candidate is decided from the bounds
+    // of its Gram distances, undecided pairs are scored exactly (eight lanes a pair)
+    const int g8 = lane >> 3, sub = lane & 7;
+    uint32_t na = 0;
+    for (uint32_t c = 0; c < nc && na < K.final_degree; ++c) {
+        const uint32_t t = sm.ci[c];
+        const float dc = sm.cd[c];
+        if (t == s)
+            continue;
+        bool sure_rej = false, unsure = false;
+        if ((uint32_t)lane < na) {
+            const uint32_t kp = sm.kpos[lane]; // kp < c
+            const float xa = sm.cn[kp], xb = sm.cn[c];
+            const float gv = sm.u.g[pg_block((int)(kp >> 5), (int)(c >> 5))][kp & 31u][c & 31u];
+            const float dt = __builtin_fmaf(-2.0f, gv, xa + xb);
+            const double nab = (double)sm.cr[kp] + (double)sm.cr[c];
+            const double ea = K.eps_coef * nab * nab;
+            const float lo_b = fmaxf(lower_bound_ea(dt, ea, K.shrink), 0.0f);
+            const float up_b = upper_bound_ea(dt, ea, K.shrink);
+            sure_rej = K.alpha * up_b < dc;
+            unsure = !sure_rej && !(K.alpha * lo_b >= dc);
+        }
+        bool reject = __ballot(sure_rej) != 0;
+        uint64_t um = __ballot(unsure);
+        // undecided kept points, eight per pass (a uniform loop)
+        while (!reject && um) {
+            uint32_t pick = NONE;
+            uint64_t mm = um;
+            for (int q = 0; q <= g8 && mm; ++q) {
+                const uint32_t f = (uint32_t)__builtin_ctzll(mm);
+                mm &= mm - 1;
+                if (q == g8)
+                    pick = f;
+            }
+            for (int q = 0; q < 8 && um; ++q)
+                um &= um - 1;
+            const bool valid = pick != NONE;
+            const uint32_t piv = valid ? sm.kept[pick] : t;
+            const float dij = l2_ref_8lane(X + (size_t)piv * K.d, X + (size_t)t * K.d, K.d, sub);
+            reject = __ballot(valid && sub == 0 && K.alpha * dij < dc) != 0;
+        }
+        if (!reject) {
+            if (lane == 0) {
+                sm.kept[na] = t;
+                sm.kpos[na] = c;
+            }
+            ++na;
+            __syncthreads();
+        }
+    }
+    uint32_t *row = K.graph + r * (K.final_degree + 1);
+    if (lane == 0)
+        row[0] = na;
+    for (uint32_t j = (uint32_t)lane; j < K.final_degree; j += 64)
+        row[1 + j] = j < na ? sm.kept[j] : s;
 }
 
 // MFMA fragment layout probe: D = A(32x2) * B(2x32) for a known A, B.

@@ -334,6 +334,13 @@ struct ung_hip_ctx {
     // test hook: UNG_HIP_EPS_SCALE=s (s >= 1) at create widens the certification error
     // bound by s, which sends more rows (all, for a huge s) through the exact rescan
     double eps_scale = 1.0;
+    // large-group prune: the certified Gram pre-decision (ung_prune_gram_kernel) from
+    // dp >= 256, where the exact alpha tests' row loads dominate (cfg4, d = 768: 272 -> 76
+    // ms; cfg3, d = 384: 21.8 -> 9.4 ms), every alpha test scored exactly (ung_prune_kernel)
+    // below (cfg2, d = 128: 12.7 against 19.8 ms).  Test hooks at create:
+    // UNG_HIP_PRUNE_EXACT=1 takes the exact scan, UNG_HIP_PRUNE_GRAM=1 the Gram kernel, at
+    // any d.
+    int prune_mode = 0; // 0: by dp, 1: exact, 2: Gram
 };
 
 namespace {
@@ -2025,6 +2032,10 @@ int ung_hip_create(int device, ung_hip_ctx **out)
         ctx->qreg = s[0] != '1';
     if (const char *s = std::getenv("UNG_HIP_NO_KNN"))
         ctx->knn = s[0] != '1';
+    if (const char *s = std::getenv("UNG_HIP_PRUNE_EXACT"); s && s[0] == '1')
+        ctx->prune_mode = 1;
+    if (const char *s = std::getenv("UNG_HIP_PRUNE_GRAM"); s && s[0] == '1')
+        ctx->prune_mode = 2;
     if (const char *s = std::getenv("UNG_HIP_EPS_SCALE")) {
         const double v = std::atof(s);
         ctx->eps_scale = v >= 1.0 ? v : 1.0; // a smaller bound would not be an error bound
@@ -2489,6 +2500,11 @@ int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t r
     K.rev_cnt = ctx->rv_cnt.p;
     K.rev_fill = ctx->rv_fill.p;
     K.graph = ctx->graph.p;
+    K.xs = ctx->XS;
+    K.xn = ctx->xn;
+    K.dp = ctx->dp;
+    K.eps_coef = eps_coef_for(ctx->d) * ctx->eps_scale;
+    K.shrink = ((double)ctx->d / 8.0 + 8.0) * std::ldexp(1.0, -24);
     HIPCHECK(hipEventRecord(ctx->ev[6], ctx->stream));
     const unsigned zb = (unsigned)std::min<uint64_t>((rows + 256) / 256, 65535);
     hipLaunchKernelGGL(ung_zero_u32_kernel, dim3(zb), dim3(256), 0, ctx->stream, ctx->rv_cnt.p, (uint32_t)(rows + 1));
@@ -2514,7 +2530,10 @@ int ung_hip_prune_group_graph(ung_hip_ctx *ctx, uint32_t forward_cap, uint32_t r
     K.rev_dist = ctx->rv_dist.p;
     hipLaunchKernelGGL(ung_reverse_kernel<true>, dim3(rb), dim3(256), 0, ctx->stream, K);
     HIPCHECK(hipGetLastError());
-    hipLaunchKernelGGL(ung_prune_kernel, dim3((unsigned)rows), dim3(64), 0, ctx->stream, K);
+    if (ctx->prune_mode == 2 || (ctx->prune_mode == 0 && ctx->dp >= 256u))
+        hipLaunchKernelGGL(ung_prune_gram_kernel, dim3((unsigned)rows), dim3(64), 0, ctx->stream, K);
+    else
+        hipLaunchKernelGGL(ung_prune_kernel, dim3((unsigned)rows), dim3(64), 0, ctx->stream, K);
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipEventRecord(ctx->ev[7], ctx->stream));
     const auto t1 = clk::now();

@@ -102,3 +102,59 @@ def test_stage_large_groups_cfg2_scaled(oracle):
         got = res.packed_graph[res.packed_offsets[i]:res.packed_offsets[i + 1]]
         assert np.array_equal(got, want), f"group {g}"
     st.close()
+
+
+def _prune_ctx(var):
+    """A context with one of the prune test hooks set: UNG_HIP_PRUNE_EXACT=1 scores every
+    alpha test exactly, UNG_HIP_PRUNE_GRAM=1 takes the certified Gram kernel at any d."""
+    import os
+    old = os.environ.get(var)
+    os.environ[var] = "1"
+    try:
+        return F.HipContext(0)
+    finally:
+        if old is None:
+            del os.environ[var]
+        else:
+            os.environ[var] = old
+
+
+@pytest.mark.parametrize("kind,dim", [("far", 128), ("far", 768), ("mixed", 64), ("int", 9), ("far", 300)])
+def test_prune_gram_matches_exact_scan(oracle, kind, dim):
+    """The certified Gram pre-decision against the exact scan of every alpha test, row for
+    row, on data that leaves many pairs undecided (tight clusters far from the origin:
+    distances far below the bound's error term; coordinates of mixed magnitudes; integer
+    data with exact ties at alpha * d == d), for alpha 1.2, 0 and 1e30, and against the
+    restatement."""
+    _say(f"prune gram vs exact scan: {kind} d={dim}")
+    rng = np.random.default_rng(40 + dim)
+    N = 3000
+    if kind == "far":
+        centres = rng.standard_normal((3, dim))
+        centres *= 100.0 / np.linalg.norm(centres, axis=1, keepdims=True)
+        X = (centres[rng.integers(0, 3, size=N)] + 0.05 * rng.standard_normal((N, dim))).astype(np.float32)
+    elif kind == "mixed":
+        X = (rng.standard_normal((N, dim)) * 10.0 ** rng.uniform(-3, 3, size=dim)).astype(np.float32)
+    else:
+        X = rng.integers(-2, 3, size=(N, dim)).astype(np.float32)
+    groups = [(0, 1800), (1800, 1200)]
+    begins = np.array([b for b, _ in groups], np.uint32)
+    sizes = np.array([n for _, n in groups], np.uint32)
+    ex, gr = _prune_ctx("UNG_HIP_PRUNE_EXACT"), _prune_ctx("UNG_HIP_PRUNE_GRAM")
+    try:
+        ex.prepare_vectors(X)
+        gr.prepare_vectors(X)
+        for alpha in (1.2, 0.0, 1e30):
+            got = []
+            for c in (gr, ex):
+                c.group_knn_device(begins, sizes, 63)
+                rows, _, _ = c.prune_group_graph(N, len(groups), 63, 32, 32, alpha)
+                got.append(rows)
+            bad = np.nonzero((got[0] != got[1]).any(1))[0]
+            assert bad.size == 0, f"{kind} d={dim} alpha={alpha}: rows {bad[:5]} differ"
+            if alpha == 1.2:
+                want = oracle.large_group_graph(X, 0, 1800, 63, 63, 32, 32, 1.2)
+                assert np.array_equal(got[0][:1800], want), f"{kind} d={dim}: restatement"
+    finally:
+        ex.close()
+        gr.close()
