@@ -108,7 +108,8 @@ __device__ __forceinline__ uint32_t cand_id(const uint32_t *__restrict__ seg_sta
 
 __device__ __forceinline__ bool cand_less(float da, uint32_t ia, float db, uint32_t ib)
 {
-    return da < db || (da == db && ia < ib);
+    // bitwise, not short-circuit: lane masks combine without branches
+    return (da < db) | ((da == db) & (ia < ib));
 }
 
 // Squared L2 with the rounding of the reference's release build of
@@ -2087,7 +2088,7 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
             for (uint32_t f = 0; f < n; ++f) {
                 const float df = __shfl(ed[0], (int)f);
                 const uint32_t idf = __shfl(eid[0], (int)f);
-                rk[0] += (df < ed[0] || (df == ed[0] && (idf < eid[0] || (idf == eid[0] && f < (uint32_t)lane)))) ? 1u : 0u;
+                rk[0] += ((df < ed[0]) | ((df == ed[0]) & ((idf < eid[0]) | ((idf == eid[0]) & (f < (uint32_t)lane))))) ? 1u : 0u;
             }
         } else {
             for (uint32_t f = 0; f < n; ++f) {
@@ -2097,7 +2098,7 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const uint32_t me = 64u * (uint32_t)h + (uint32_t)lane;
-                    rk[h] += (df < ed[h] || (df == ed[h] && (idf < eid[h] || (idf == eid[h] && f < me)))) ? 1u : 0u;
+                    rk[h] += ((df < ed[h]) | ((df == ed[h]) & ((idf < eid[h]) | ((idf == eid[h]) & (f < me))))) ? 1u : 0u;
                 }
             }
         }
@@ -2296,7 +2297,7 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t me = 64u * (uint32_t)h + (uint32_t)lane;
-            rank[h] += (df < ex[h] || (df == ex[h] && (idf < ci[h] || (idf == ci[h] && f < me)))) ? 1u : 0u;
+            rank[h] += ((df < ex[h]) | ((df == ex[h]) & ((idf < ci[h]) | ((idf == ci[h]) & (f < me))))) ? 1u : 0u;
         }
     }
     bool mine[2], real[2];
