@@ -192,7 +192,8 @@ __amd_rocclr_copyBuffer, 1,048,576 KiB read and 1,048,576 KiB written):
   FETCH_SIZE reads {fc:,.1f} KiB -> scale {fs:.4f} (1,048,576 / {fc:,.1f})
   WRITE_SIZE reads {wc:,.1f} KiB -> scale {ws:.4f}
 
-Select kernel (first of the {nsel} cross select dispatches of each pass: dispatch {fdisp} / {wdisp}):
+Select kernel (the first of each pass's {nsel} cross select dispatches: Dispatch_Id {fdisp} in the
+FETCH_SIZE pass, {wdisp} in the WRITE_SIZE pass):
   FETCH_SIZE {fk:,.1f} KiB x {fs:.4f} = {int(fb):,} B
   WRITE_SIZE {wk:,.1f} KiB x {ws:.4f} = {int(wb):,} B
   duration {fd:.2f} ms (FETCH pass) / {wd:.2f} ms (WRITE pass), counters serialize the dispatches

@@ -124,8 +124,10 @@ def test_prune_gram_matches_exact_scan(oracle, kind, dim):
     """The certified Gram pre-decision against the exact scan of every alpha test, row for
     row, on data that leaves many pairs undecided (tight clusters far from the origin:
     distances far below the bound's error term; coordinates of mixed magnitudes; integer
-    data with exact ties at alpha * d == d), for alpha 1.2, 0 and 1e30, and against the
-    restatement."""
+    data with exact ties at alpha * d == d), for alpha 1.2, 0, 1e30 and +inf (inf * 0 is NaN:
+    a pair at distance 0 stays undecided and is scored exactly), with groups of 40 and 10
+    points (rows with fewer candidates than one 32-row block of the Gram matrix), and
+    against the restatement."""
     _say(f"prune gram vs exact scan: {kind} d={dim}")
     rng = np.random.default_rng(40 + dim)
     N = 3000
@@ -137,14 +139,15 @@ def test_prune_gram_matches_exact_scan(oracle, kind, dim):
         X = (rng.standard_normal((N, dim)) * 10.0 ** rng.uniform(-3, 3, size=dim)).astype(np.float32)
     else:
         X = rng.integers(-2, 3, size=(N, dim)).astype(np.float32)
-    groups = [(0, 1800), (1800, 1200)]
+    X[2000] = X[1900]  # an exact duplicate: d(kept, candidate) = 0
+    groups = [(0, 1800), (1800, 1150), (2950, 40), (2990, 10)]
     begins = np.array([b for b, _ in groups], np.uint32)
     sizes = np.array([n for _, n in groups], np.uint32)
     ex, gr = _prune_ctx("UNG_HIP_PRUNE_EXACT"), _prune_ctx("UNG_HIP_PRUNE_GRAM")
     try:
         ex.prepare_vectors(X)
         gr.prepare_vectors(X)
-        for alpha in (1.2, 0.0, 1e30):
+        for alpha in (1.2, 0.0, 1e30, np.inf):
             got = []
             for c in (gr, ex):
                 c.group_knn_device(begins, sizes, 63)
@@ -155,6 +158,8 @@ def test_prune_gram_matches_exact_scan(oracle, kind, dim):
             if alpha == 1.2:
                 want = oracle.large_group_graph(X, 0, 1800, 63, 63, 32, 32, 1.2)
                 assert np.array_equal(got[0][:1800], want), f"{kind} d={dim}: restatement"
+                want = oracle.large_group_graph(X, 2950, 40, 63, 63, 32, 32, 1.2)
+                assert np.array_equal(got[0][2950:2990], want), f"{kind} d={dim}: restatement, 40 points"
     finally:
         ex.close()
         gr.close()
