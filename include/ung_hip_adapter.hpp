@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <exception>
 #include <limits>
 #include <stdexcept>
 #include <string>
@@ -111,18 +112,35 @@ class Backend {
                                         &last_),
                  "cross_groups_search_all_batched (download)");
         if (id_vectors) {
-            // IdVector writeback, rows filled in parallel
+            // IdVector writeback, rows filled in parallel (part 0 on this thread; an
+            // exception of any part is rethrown here after every thread has joined)
             id_vectors->assign(N, {});
             const uint32_t *src = ids->data();
             const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-            std::vector<std::thread> pool;
-            for (unsigned t = 0; t < nt; ++t)
-                pool.emplace_back([&, t] {
+            std::vector<std::exception_ptr> err(nt);
+            auto fill = [&](unsigned t) {
+                try {
                     for (uint64_t p = N * t / nt; p < N * (t + 1) / nt; ++p)
                         (*id_vectors)[p].assign(src + p * k_, src + p * k_ + sizes_[p]);
-                });
+                } catch (...) {
+                    err[t] = std::current_exception();
+                }
+            };
+            std::vector<std::thread> pool;
+            pool.reserve(nt);
+            for (unsigned t = 1; t < nt; ++t) {
+                try {
+                    pool.emplace_back(fill, t);
+                } catch (...) {
+                    fill(t); // no thread to spare: this part runs here
+                }
+            }
+            fill(0);
             for (auto &th : pool)
                 th.join();
+            for (const auto &e : err)
+                if (e)
+                    std::rethrow_exception(e);
         }
     }
 

@@ -10,13 +10,15 @@
   - every cross row: size = min(k, |union|), padding, (dist, id) order, every id inside
     the row's minimum-superset union, and every distance bit-exact against the reference's
     summation order (oracle ungo_l2_pairs, pinned against the compiled reference);
-  - every row the certificate sent to the exact rescan, plus a large random sample of
-    rows, bit-exact against the reference's compiled distance + SearchQueue scan
-    (oracle/_ref, else the plain-C oracle);
+  - every row the certificate sent to the exact rescan, plus (cfg3) every other row or
+    (cfg4: 200,000 rows, cfg5: 30,000; all their rows would take 2.5e13 and 2.6e14
+    multiply-adds, minutes to an hour on the box's CPUs) a random sample of rows,
+    bit-exact against the reference's compiled distance + SearchQueue scan (oracle/_ref,
+    else the plain-C oracle);
   - the additional edges of every group (a random sample when the oracle's scan would
     exceed its budget) against the oracle fed the GPU's cross rows;
   - every intra row (mid groups, K = 32): size, local ids, no self, (dist, id) order,
-    distances bit-exact; every rescanned intra row and a sample of groups bit-exact.
+    distances bit-exact; every group's lists bit-exact against the reference.
 """
 import hashlib
 
@@ -140,7 +142,10 @@ def _full_size(cfg_name, oracle, n_cross_sample, n_intra_groups, addl_budget_dim
     rescanned = ctx.rescanned_rows(0)
     assert rescanned.size == stats["fallback_rows"]
     eligible = np.nonzero(union[pg] > 0)[0]
-    sample = rng.choice(eligible, size=min(n_cross_sample, eligible.size), replace=False)
+    if n_cross_sample is None:  # every row with a non-empty union
+        sample = eligible
+    else:
+        sample = rng.choice(eligible, size=min(n_cross_sample, eligible.size), replace=False)
     q = np.union1d(sample, rescanned).astype(np.uint32)
     _say(f"{cfg_name} full: {q.size} rows ({rescanned.size} rescanned) against the reference scan")
     res = chk.cross_exact_points(st.base, st.group_begin, pg, st.out_ptr, st.out_idx, q, k)
@@ -201,7 +206,10 @@ def _full_size(cfg_name, oracle, n_cross_sample, n_intra_groups, addl_budget_dim
                 np.minimum(K, n_row - 1))
     rescanned = ctx.rescanned_rows(1)
     assert rescanned.size == kst["fallback_rows"]
-    pick_g = set(rng.choice(gids.size, size=min(n_intra_groups, gids.size), replace=False).tolist())
+    if n_intra_groups is None:  # every mid group
+        pick_g = set(range(gids.size))
+    else:
+        pick_g = set(rng.choice(gids.size, size=min(n_intra_groups, gids.size), replace=False).tolist())
     pick_g |= set(row_grp[rescanned].tolist())
     _say(f"{cfg_name} full: {len(pick_g)} groups ({rescanned.size} rescanned rows) against the reference")
     starts = np.cumsum(gsz) - gsz
@@ -213,12 +221,15 @@ def _full_size(cfg_name, oracle, n_cross_sample, n_intra_groups, addl_budget_dim
 
 
 def test_cfg3_full_size(oracle):
-    _full_size("cfg3", oracle, n_cross_sample=50_000, n_intra_groups=40, addl_budget_dims=2e10)
+    # every cross row (5.9e9 pairs at d = 384) and every mid group against the reference
+    _full_size("cfg3", oracle, n_cross_sample=None, n_intra_groups=None, addl_budget_dims=2e10)
 
 
 def test_cfg4_full_size(oracle):
-    _full_size("cfg4", oracle, n_cross_sample=20_000, n_intra_groups=30, addl_budget_dims=2e10)
+    # a tenth of the cross rows (every row: 2.5e13 multiply-adds) and every mid group
+    _full_size("cfg4", oracle, n_cross_sample=200_000, n_intra_groups=None, addl_budget_dims=2e10)
 
 
 def test_cfg5_full_size(oracle):
-    _full_size("cfg5", oracle, n_cross_sample=10_000, n_intra_groups=30, addl_budget_dims=2e10)
+    # 30,000 cross rows (every row: 2.6e14 multiply-adds) and every mid group
+    _full_size("cfg5", oracle, n_cross_sample=30_000, n_intra_groups=None, addl_budget_dims=2e10)
