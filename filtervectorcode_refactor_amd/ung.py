@@ -432,11 +432,14 @@ class UngBuildStage:
     configs), ``tagore_k`` (UNG_TAGORE_K, default 64, src/ung_build_config.cpp:341),
     ``tagore_min_group_size`` / ``exact_max_nx`` (mid-group range 128..4096,
     src/ung_build_config.cpp:339, src/ung_build_settings.cpp:246-252), ``alpha`` (the
-    prune factor, include/config.h)."""
+    prune factor, include/config.h), ``scenario`` (the build's --scenario,
+    apps/build_UNG_index.cpp:52, default "general"; "equality" builds no label navigating
+    graph and no cross edges, src/uni_nav_graph.cpp:95-99)."""
 
     def __init__(self, num_cross_edges: int = 6, max_degree: int = 32, tagore_k: int = 64,
                  tagore_min_group_size: int = 128, exact_max_nx: int = 4096, device: int = 0,
-                 num_threads: int = 0, alpha: float = 1.2):
+                 num_threads: int = 0, alpha: float = 1.2, scenario: str = "general"):
+        self.scenario = str(scenario)
         self.num_cross_edges = int(num_cross_edges)
         self.max_degree = int(max_degree)
         self.alpha = float(alpha)
@@ -478,12 +481,26 @@ class UngBuildStage:
         self.out_ptr, self.out_idx = lng_build(set_ptr, set_idx, self.num_threads)
         self.in_ptr, self.in_idx = in_neighbors(self.out_ptr, self.out_idx)
 
+    def skip_label_nav_graph(self):
+        """The "equality" scenario (src/uni_nav_graph.cpp:95-99): no label navigating graph,
+        so every group's LNG row is empty -- the cross-edge call then returns padding rows
+        only, the additional edges are empty, and the assembled graph holds the intra edges
+        with add_offset_for_uni_nav_graph, as the reference's build does."""
+        G = self.num_groups
+        self.out_ptr = np.zeros(G + 2, np.uint32)
+        self.out_idx = np.zeros(0, np.uint32)
+        self.in_ptr = np.zeros(G + 2, np.uint32)
+        self.in_idx = np.zeros(0, np.uint32)
+
     def prepare_inputs(self, X, lab_ptr, lab_idx):
         """Steps 2, 3 and 7 of UniNavGraph::build (src/uni_nav_graph.cpp:54-146)."""
         self.load_arrays(X, lab_ptr, lab_idx)
         self.build_trie_and_divide_groups()
         self.prepare_group_storages_graphs()
-        self.build_label_nav_graph()
+        if self.scenario == "equality":
+            self.skip_label_nav_graph()
+        else:
+            self.build_label_nav_graph()
 
     # ---- device -------------------------------------------------------------
     @property

@@ -402,6 +402,40 @@ def test_pipeline_graph_cfg1(cfg1_stage, oracle, tmp_path):
     st.close()
 
 
+def test_pipeline_equality_scenario_cfg1(oracle):
+    """The "equality" scenario end to end on cfg1 (src/uni_nav_graph.cpp:95-99): the
+    cross-edge call returns padding rows only, there are no additional edges, and the graph
+    holds the intra rows with add_offset only."""
+    from filtervectorcode_refactor_amd import datasets as D
+    X, lp, li = D.generate(D.CONFIGS["cfg1"])
+    st = F.UngBuildStage(scenario="equality")
+    st.prepare_inputs(X, lp, li)
+    st.gpu_prepare_all_vectors_on_device()
+    ids, dist, size = st.gpu_cross_groups_search_all_batched()
+    assert (ids == 0xFFFFFFFF).all() and np.isinf(dist).all() and not size.any()
+    ptr_, ef, et = st.build_cross_edges_generate_additional()
+    assert ef.size == 0 and et.size == 0 and not ptr_.any()
+    batch = st.build_fast_exact_batch()
+    N = int(st.group_begin[-1])
+    deg = np.zeros(N, np.int64)
+    rows = {}
+    r = 0
+    for g in st.mid_groups():
+        b, n = int(st.group_begin[g]), int(st.group_begin[g + 1] - st.group_begin[g])
+        for j in range(n):
+            row = batch.packed_graph[r + j]
+            rows[b + j] = row[1: 1 + row[0]]
+            deg[b + j] = row[0]
+        r += n
+    ip = np.zeros(N + 1, np.uint64)
+    ip[1:] = np.cumsum(deg)
+    ii = np.concatenate([rows[i] for i in sorted(rows)]).astype(np.uint32)
+    rp, ci = st.build_csr_adjacency(ip, ii)
+    wrp, wci = oracle.assemble_graph(N, st.group_begin, ip, ii, False, None, 0, None, None, None)
+    assert np.array_equal(rp, wrp) and np.array_equal(ci, wci)
+    st.close()
+
+
 def test_cross_intra_overlapped_equals_sequential(ctx, oracle):
     """ung_hip_cross_intra_begin / ung_hip_intra_end (cross edges and the mid groups' kNN
     on two streams, additional edges in between) give the rows of the sequential calls,

@@ -295,6 +295,24 @@ def test_assemble_graph_matches_reference_container(oracle, ref_oracle, cfg1_sta
     assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
 
 
+def test_equality_scenario_skips_lng(oracle, cfg1_stage):
+    """The "equality" scenario (src/uni_nav_graph.cpp:95-99): the same groups and reorder,
+    empty LNG rows, and a graph of the intra edges with add_offset only."""
+    from filtervectorcode_refactor_amd import datasets as D
+    X, lp, li = D.generate(D.CONFIGS["cfg1"])
+    st = F.UngBuildStage(scenario="equality")
+    st.prepare_inputs(X, lp, li)
+    ref = cfg1_stage
+    assert st.num_groups == ref.num_groups and np.array_equal(st.group_begin, ref.group_begin)
+    assert np.array_equal(st.base, ref.base)
+    assert not st.out_ptr.any() and st.out_idx.size == 0 and not st.in_ptr.any() and st.in_idx.size == 0
+    N, ip, ii, _, _ = _graph_inputs(oracle, ref, np.random.default_rng(6))
+    rp, ci = st.build_csr_adjacency(ip, ii)
+    want = oracle.assemble_graph(N, st.group_begin, ip, ii, False, None, 0, None, None, None)
+    assert np.array_equal(rp, want[0]) and np.array_equal(ci, want[1])
+    assert np.array_equal(np.diff(rp.astype(np.int64)), np.diff(ip.astype(np.int64)))
+
+
 def test_assemble_graph_hand_worked():
     gb = np.array([0, 0, 2, 3], np.uint32)           # group 1 = {0, 1}, group 2 = {2}
     ip = np.array([0, 1, 2, 2], np.uint64)           # 0 -> local 1, 1 -> local 0
