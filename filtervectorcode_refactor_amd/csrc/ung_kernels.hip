@@ -40,6 +40,7 @@ constexpr int NTHREADS = 256;    // 4 waves: 2 (candidate halves) x 2 (query hal
 constexpr uint32_t SPLIT_V = 32768; // candidates per work item (raised so a job has <= 64 splits)
 constexpr uint32_t MAX_SPLITS = 64; // one wave lane per split in the merge
 constexpr uint32_t MERGE_ROWS = 4;  // result rows (one wave each) per merge block
+constexpr uint32_t MERGE_QLDS = 1024; // largest d whose query rows the merge stages in LDS
 constexpr uint32_t MERGE_Q = 256;   // rows per packing block
 constexpr uint32_t NONE = 0xFFFFFFFFu;
 
@@ -1983,6 +1984,7 @@ struct MergeParams {
     uint2 *flagged;
     uint32_t n_mitems;   // items of this launch
     uint32_t xcd_spread; // 1: consecutive items to one XCD (see ung_merge_kernel)
+    uint32_t qlds;       // 1: the launch gave MERGE_ROWS * d floats of LDS for query rows
 };
 
 // The MI355X's XCDs; the dispatcher hands a launch's workgroups to them round-robin.
@@ -2206,56 +2208,72 @@ __global__ __launch_bounds__(64 * MERGE_ROWS) void ung_merge_kernel(MergeParams 
 
     // exact re-score: 8 lanes per candidate (one per accumulator of the reference's
     // summation), 8 candidates per pass (PAIR: 16); candidate t's value goes to lane
-    // t % 64, slot t / 64
-    const float *qv = M.X + (size_t)q * M.d;
+    // t % 64, slot t / 64.  Rows of more than two passes read the query row from a copy
+    // in this wave's LDS slice when the launch gave one (group kNN merges, d <=
+    // MERGE_QLDS), so that every pass loads only the candidates' rows from memory (~33
+    // candidates: cfg4 7.8 -> 6.2 ms, cfg2 0.71 -> 0.67 ms).  The arithmetic is the same
+    // either way.
     float ex[2] = {INFINITY, INFINITY};
-    if constexpr (PAIR) {
-        // group g scores candidates 16p + g and 16p + 8 + g (t < 128: Lp <= 128); lane L
-        // takes candidate 8 (2p + e) + L % 8 from group L % 8, e = 0, 1
-        const int g = lane >> 3, sub = lane & 7;
-        const uint32_t npass = (m_need + 15u) / 16u;
-        for (uint32_t p = 0; p < npass; ++p) {
-            const uint32_t t0 = 16u * p + (uint32_t)g, t1 = t0 + 8u;
-            const uint32_t c0 = t0 < 64u ? __shfl(ci[0], (int)(t0 & 63u)) : __shfl(ci[1], (int)(t0 & 63u));
-            const uint32_t c1 = t1 < 64u ? __shfl(ci[0], (int)(t1 & 63u)) : __shfl(ci[1], (int)(t1 & 63u));
-            const bool ok0 = t0 < Lp && c0 != NONE, ok1 = t1 < Lp && c1 != NONE;
-            float v0, v1 = INFINITY;
-            if (16u * p + 8u < m_need) // wave-uniform: the pass's second half holds candidates
-                l2_ref_8lane2(qv, M.X + (size_t)(ok0 ? c0 : q) * M.d, M.X + (size_t)(ok1 ? c1 : q) * M.d, M.d,
-                              sub, v0, v1);
-            else
-                v0 = l2_ref_8lane(qv, M.X + (size_t)(ok0 ? c0 : q) * M.d, M.d, sub);
-            const float got0 = __shfl(v0, 8 * (lane & 7)), got1 = __shfl(v1, 8 * (lane & 7));
+    auto rescore = [&](const float *qv) __attribute__((always_inline)) {
+        if constexpr (PAIR) {
+            // group g scores candidates 16p + g and 16p + 8 + g (t < 128: Lp <= 128); lane L
+            // takes candidate 8 (2p + e) + L % 8 from group L % 8, e = 0, 1
+            const int g = lane >> 3, sub = lane & 7;
+            const uint32_t npass = (m_need + 15u) / 16u;
+            for (uint32_t p = 0; p < npass; ++p) {
+                const uint32_t t0 = 16u * p + (uint32_t)g, t1 = t0 + 8u;
+                const uint32_t c0 = t0 < 64u ? __shfl(ci[0], (int)(t0 & 63u)) : __shfl(ci[1], (int)(t0 & 63u));
+                const uint32_t c1 = t1 < 64u ? __shfl(ci[0], (int)(t1 & 63u)) : __shfl(ci[1], (int)(t1 & 63u));
+                const bool ok0 = t0 < Lp && c0 != NONE, ok1 = t1 < Lp && c1 != NONE;
+                float v0, v1 = INFINITY;
+                if (16u * p + 8u < m_need) // wave-uniform: the pass's second half holds candidates
+                    l2_ref_8lane2(qv, M.X + (size_t)(ok0 ? c0 : q) * M.d, M.X + (size_t)(ok1 ? c1 : q) * M.d, M.d,
+                                  sub, v0, v1);
+                else
+                    v0 = l2_ref_8lane(qv, M.X + (size_t)(ok0 ? c0 : q) * M.d, M.d, sub);
+                const float got0 = __shfl(v0, 8 * (lane & 7)), got1 = __shfl(v1, 8 * (lane & 7));
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t pp = 2u * p + (uint32_t)e; // candidates 8pp .. 8pp + 7
-                if ((uint32_t)g == (pp & 7u)) {
-                    const float got = e == 0 ? got0 : got1;
-                    if (pp < 8u)
+                for (int e = 0; e < 2; ++e) {
+                    const uint32_t pp = 2u * p + (uint32_t)e; // candidates 8pp .. 8pp + 7
+                    if ((uint32_t)g == (pp & 7u)) {
+                        const float got = e == 0 ? got0 : got1;
+                        if (pp < 8u)
+                            ex[0] = ci[0] != NONE ? got : INFINITY;
+                        else
+                            ex[1] = ci[1] != NONE ? got : INFINITY;
+                    }
+                }
+            }
+        } else {
+            const int g = lane >> 3, sub = lane & 7;
+            const uint32_t npass = (m_need + 7u) / 8u;
+            for (uint32_t p = 0; p < npass; ++p) {
+                const uint32_t t = 8u * p + (uint32_t)g;
+                const int src = (int)(t & 63u);
+                const uint32_t c = t < 64u ? __shfl(ci[0], src) : __shfl(ci[1], src);
+                const bool ok = t < Lp && c != NONE;
+                const float v = l2_ref_8lane(qv, M.X + (size_t)(ok ? c : q) * M.d, M.d, sub);
+                const float got = __shfl(v, 8 * (lane & 7)); // candidate 8p + (lane % 8)
+                const uint32_t pl = p & 7u;
+                if ((uint32_t)g == pl) {
+                    if (p < 8u)
                         ex[0] = ci[0] != NONE ? got : INFINITY;
                     else
                         ex[1] = ci[1] != NONE ? got : INFINITY;
                 }
             }
         }
+    };
+    if (M.qlds && m_need > 16u) { // (m_need is wave-uniform)
+        extern __shared__ float mq[]; // [MERGE_ROWS][d], sized by the launch
+        float *const qs = mq + (size_t)w * M.d;
+        const float *const qg = M.X + (size_t)q * M.d;
+        for (uint32_t i = (uint32_t)lane; i < M.d; i += 64u)
+            qs[i] = qg[i];
+        __builtin_amdgcn_wave_barrier(); // (a wave's LDS accesses execute in order)
+        rescore(qs);
     } else {
-        const int g = lane >> 3, sub = lane & 7;
-        const uint32_t npass = (m_need + 7u) / 8u;
-        for (uint32_t p = 0; p < npass; ++p) {
-            const uint32_t t = 8u * p + (uint32_t)g;
-            const int src = (int)(t & 63u);
-            const uint32_t c = t < 64u ? __shfl(ci[0], src) : __shfl(ci[1], src);
-            const bool ok = t < Lp && c != NONE;
-            const float v = l2_ref_8lane(qv, M.X + (size_t)(ok ? c : q) * M.d, M.d, sub);
-            const float got = __shfl(v, 8 * (lane & 7)); // candidate 8p + (lane % 8)
-            const uint32_t pl = p & 7u;
-            if ((uint32_t)g == pl) {
-                if (p < 8u)
-                    ex[0] = ci[0] != NONE ? got : INFINITY;
-                else
-                    ex[1] = ci[1] != NONE ? got : INFINITY;
-            }
-        }
+        rescore(M.X + (size_t)q * M.d);
     }
     const size_t orow = (size_t)jb.out_row + ql;
     const float Bx = lower_bound_ea(B, ea, M.shrink);

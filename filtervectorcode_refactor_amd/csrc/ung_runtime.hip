@@ -677,6 +677,12 @@ void stage_plan(ung_hip_ctx *ctx, const Plan &pl, const StageLayout &L, char *hs
     });
 }
 
+// Dynamic LDS of a merge launch: the query row of each of its waves when d allows.
+size_t merge_qlds_bytes(uint32_t d)
+{
+    return d <= MERGE_QLDS ? (size_t)MERGE_ROWS * d * sizeof(float) : 0;
+}
+
 // Runs a planned job list on workspace `ws` (its stream and events) with the memory of
 // `m`; result rows already initialised by the caller when some rows have no job.
 // plan_launch uploads the work lists and enqueues the select and merge kernels;
@@ -816,6 +822,10 @@ int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t 
     // two candidates per re-score pass for group kNN rows of d >= 256 (cfg3 intra merge
     // 1.28 -> 1.14 ms, cfg4 8.58 -> 7.71 ms; at d = 128 and in the cross merge slower)
     const bool pair = group_plan && ctx->d >= 256;
+    // group kNN rows (~33 re-scored candidates) read the query row from LDS; the cross
+    // merge's short rows do not (the copy costs them more than it saves)
+    const size_t qlds = group_plan ? merge_qlds_bytes(ctx->d) : 0;
+    M.qlds = qlds ? 1u : 0u;
     const uint32_t n_m = (uint32_t)pl.n_mitems;
     for (uint32_t off = 0; off < n_m; off += (1u << 30)) {
         MergeParams Mc = M;
@@ -824,9 +834,9 @@ int plan_launch_merge(ung_hip_ctx *ctx, Workspace &ws, const Plan &pl, uint32_t 
         Mc.n_mitems = n;
         const uint32_t grid = M.xcd_spread ? NUM_XCD * ((n + NUM_XCD - 1u) / NUM_XCD) : n;
         if (pair)
-            hipLaunchKernelGGL(ung_merge_kernel<true>, dim3(grid), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
+            hipLaunchKernelGGL(ung_merge_kernel<true>, dim3(grid), dim3(64 * MERGE_ROWS), qlds, ws.stream, Mc);
         else
-            hipLaunchKernelGGL(ung_merge_kernel<false>, dim3(grid), dim3(64 * MERGE_ROWS), 0, ws.stream, Mc);
+            hipLaunchKernelGGL(ung_merge_kernel<false>, dim3(grid), dim3(64 * MERGE_ROWS), qlds, ws.stream, Mc);
         HIPCHECK(hipGetLastError());
     }
     HIPCHECK(hipEventRecord(ws.ev[2], ws.stream));
