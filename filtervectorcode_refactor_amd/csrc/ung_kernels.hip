@@ -944,8 +944,19 @@ __global__ __launch_bounds__(select_threads<NB>(), (LT <= 8 ? 2 : 1)) void ung_s
             }
         };
         // the MFMA block at raised wave priority: the SIMD's other wave (in its epilogue's
-        // VALU work) yields issue slots to it, which keeps the matrix core fed
-        __builtin_amdgcn_s_setprio(1);
+        // VALU work) yields issue slots to it, which keeps the matrix core fed.  In the
+        // register-query layout the priority also grows with the chunk (1, 2, 3, 3): of
+        // two waves in their MFMA steps, the one nearer its epilogue issues first, so it
+        // reaches the epilogue while the other still has matrix work.  Their phases drift
+        // apart instead of locking (cfg2 cross select -1.5 to 2 %).  With restaged query
+        // panels (12 to 24 chunks a tile) a graded priority measured slower, so those
+        // steps stay at 1.
+        if constexpr (QR) {
+            constexpr uint32_t KCP = decltype(kcv)::value + 1u;
+            __builtin_amdgcn_s_setprio(KCP > 3u ? 3 : (int16_t)KCP);
+        } else {
+            __builtin_amdgcn_s_setprio(1);
+        }
         if (kc == 0)
             mfma_chunk(std::true_type{});
         else
